@@ -1,0 +1,243 @@
+// Device primitives for the gfx950 sampling kernels (wave64).
+//
+// Keys: float_key is the order-preserving map of shaders/fg_topk_select.comp:27-31
+// (NaN/Inf -> 0; +0 above -0).  A candidate is carried as one 64-bit
+// "composite" (key << 32) | ~id: ids are unique within a row, so composites
+// are unique and their unsigned order is exactly the top-k order of the
+// reference's select ladder (key desc, then lower id first).  Composite 0 (and
+// anything below 2^32) means "no candidate".
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fg {
+
+constexpr int kWave = 64;
+constexpr uint32_t kInvalidId = 0xffffffffu;
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t lane_id() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+// Number of set bits of `mask` below this lane.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+// Orders LDS traffic between lanes of one wave: LDS executes a wave's
+// operations in issue order, so a compiler fence at wavefront scope suffices.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+__device__ __forceinline__ bool is_finite_bits(uint32_t b) {
+  return (b & 0x7f800000u) != 0x7f800000u;
+}
+
+__device__ __forceinline__ uint32_t float_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  if (!is_finite_bits(b)) return 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ uint64_t make_comp(uint32_t key, uint32_t id) {
+  return (static_cast<uint64_t>(key) << 32) | static_cast<uint64_t>(~id);
+}
+__device__ __forceinline__ uint32_t comp_key(uint64_t c) { return static_cast<uint32_t>(c >> 32); }
+__device__ __forceinline__ uint32_t comp_id(uint64_t c) { return ~static_cast<uint32_t>(c); }
+
+// Greedy order of src/output.c:484-492 as one 64-bit max: non-finite values
+// rank first (hi = all ones), finite ones by key with -0 folded onto +0 (the
+// reference compares values, so 0 == -0 and the lower id wins), ties by lower
+// id (lo = ~id).  Padding ids encode as 0 and lose to everything.
+__device__ __forceinline__ uint64_t greedy_comp(float v, uint32_t id) {
+  if (id == kInvalidId) return 0ull;
+  uint32_t b = __float_as_uint(v);
+  uint32_t hi;
+  if (!is_finite_bits(b)) {
+    hi = 0xffffffffu;
+  } else {
+    if (b == 0x80000000u) b = 0u;
+    hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(~id);
+}
+
+// Penalty of src/sampler.c:55-58 for one logit seen c > 0 times.  The kernels
+// are compiled with -ffp-contract=off so the product and the sum round
+// separately, and '/' is the IEEE-rounded f32 division.
+__device__ __forceinline__ float penalise(float s, uint32_t c, float pres, float freq, float rep) {
+  if (c == 0u) return s;
+  if (rep != 1.0f) s = s > 0.0f ? s / rep : s * rep;
+  const float fc = freq * static_cast<float>(c);
+  const float total = fc + pres;
+  return s - total;
+}
+
+// ---- wave reductions --------------------------------------------------------
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint64_t o = __shfl_xor(v, d);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint64_t o = __shfl_xor(v, d);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+  return v;
+}
+
+// Inclusive sum over lanes >= this lane.
+__device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t v) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = __shfl_down(v, d);
+    if (lane + d < kWave) v += o;
+  }
+  return v;
+}
+
+// Bitonic sort of one u64 per lane across the wave, descending (lane 0 holds
+// the largest).
+__device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t v) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j >= 1; j >>= 1) {
+      const uint64_t o = __shfl_xor(v, j);
+      // Within each k-block the final stage runs descending; blocks alternate.
+      const bool desc = ((lane & k) == 0);
+      const bool lower = ((lane & j) == 0);
+      const bool take_max = (lower == desc);
+      const uint64_t hi = o > v ? o : v;
+      const uint64_t lo = o > v ? v : o;
+      v = take_max ? hi : lo;
+    }
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j >= 1; j >>= 1) {
+      const uint32_t o = __shfl_xor(v, j);
+      const bool desc = ((lane & k) == 0);
+      const bool lower = ((lane & j) == 0);
+      const bool take_max = (lower == desc);
+      v = take_max ? (o > v ? o : v) : (o > v ? v : o);
+    }
+  }
+  return v;
+}
+
+// ---- exact k-th largest composite over an LDS array, one wave -------------
+//
+// MSB-first radix select, 8 bits per round, on n unique composites in
+// buf[0..n).  Requires 1 <= kk <= n.  Returns the kk-th largest composite R;
+// exactly kk entries satisfy c >= R.  hist is 256 u32 of wave-private LDS.
+__device__ inline uint64_t wave_select_kth(const uint64_t* buf, uint32_t n, uint32_t kk,
+                                           uint32_t* hist) {
+  const uint32_t lane = lane_id();
+  uint64_t prefix = 0;
+  uint32_t need = kk;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (uint32_t b = lane; b < 256u; b += kWave) hist[b] = 0u;
+    wave_lds_sync();
+    const uint64_t hi_mask = (shift == 56) ? 0ull : (~0ull << (shift + 8));
+    for (uint32_t i = lane; i < n; i += kWave) {
+      const uint64_t c = buf[i];
+      if ((c & hi_mask) == prefix) atomicAdd(&hist[(c >> shift) & 255u], 1u);
+    }
+    wave_lds_sync();
+    uint32_t h[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) h[q] = hist[4u * lane + q];
+    wave_lds_sync();
+    const uint32_t mine = h[0] + h[1] + h[2] + h[3];
+    const uint32_t suf = wave_suffix_sum(mine);
+    uint32_t above = suf - mine;
+    const bool owner = above < need && need <= suf;
+    uint32_t bin = 0, bin_above = 0, bin_count = 0;
+    if (owner) {
+#pragma unroll
+      for (int q = 3; q >= 0; q--) {
+        if (above + h[q] >= need) {
+          bin = 4u * lane + q;
+          bin_above = above;
+          bin_count = h[q];
+          break;
+        }
+        above += h[q];
+      }
+    }
+    const uint64_t who = ballot(owner);
+    const int src = __ffsll(static_cast<unsigned long long>(who)) - 1;
+    bin = __shfl(bin, src);
+    bin_above = __shfl(bin_above, src);
+    bin_count = __shfl(bin_count, src);
+    prefix |= static_cast<uint64_t>(bin) << shift;
+    need -= bin_above;
+    if (bin_count == need) {
+      // Every entry of this bucket is in: the answer is the smallest entry
+      // whose bits down to `shift` are >= prefix.
+      uint64_t best = ~0ull;
+      for (uint32_t i = lane; i < n; i += kWave) {
+        const uint64_t c = buf[i];
+        if (c >= prefix && c < best) best = c;
+      }
+      return wave_min_u64(best);
+    }
+  }
+  return prefix;  // not reached: a bucket of one unique composite ends the loop
+}
+
+// Keeps the entries c >= R of buf[0..n) at the front, in their current order;
+// returns how many were kept.
+__device__ inline uint32_t wave_compact_ge(uint64_t* buf, uint32_t n, uint64_t R) {
+  const uint32_t lane = lane_id();
+  uint32_t kept = 0;
+  for (uint32_t base = 0; base < n; base += kWave) {
+    const uint32_t i = base + lane;
+    const uint64_t c = i < n ? buf[i] : 0ull;
+    const bool keep = i < n && c >= R;
+    const uint64_t m = ballot(keep);
+    wave_lds_sync();
+    if (keep) buf[kept + lanes_below(m)] = c;
+    wave_lds_sync();
+    kept += __popcll(m);
+  }
+  return kept;
+}
+
+}  // namespace fg

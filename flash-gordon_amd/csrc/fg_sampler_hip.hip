@@ -1,0 +1,310 @@
+// extern "C" entry points of include/fg_sampler_hip.h: argument checks,
+// launch shapes and workspace ownership for the gfx950 sampling kernels.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "fg_sampler_hip.h"
+#include "fg_sample_kernels.hpp"
+#include "fg_unit_kernels.hpp"
+
+namespace {
+
+using fg::RowParams;
+
+__device__ uint32_t g_history_bad;  // set by history_count_kernel on an id >= vocab
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+fg_status hip_fail(fg_error* err, hipError_t e, const char* what) {
+  fg_error_set(err, FG_ERR_UNAVAILABLE, "%s: %s", what, hipGetErrorString(e));
+  return FG_ERR_UNAVAILABLE;
+}
+
+fg_status arg_fail(fg_error* err, const char* msg) {
+  fg_error_set(err, FG_ERR_ARGUMENT, "%s", msg);
+  return FG_ERR_ARGUMENT;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Validation of src/sampler.c:24-38, with top_k == 0 admitted when the
+// whole-vocabulary extension is enabled.
+bool config_ok(const fg_sampler_config* c, uint32_t flags) {
+  if (c->top_k == 0u && (flags & FG_SAMPLER_HIP_ALLOW_FULL_VOCAB)) {
+    fg_sampler_config probe = *c;
+    probe.top_k = 1u;
+    return fg_sampler_config_validate(&probe, nullptr) == FG_OK;
+  }
+  return fg_sampler_config_validate(c, nullptr) == FG_OK;
+}
+
+}  // namespace
+
+struct fg_sampler_hip {
+  int device;
+  uint32_t vocab;
+  uint32_t max_rows;
+  RowParams* d_params;      // [max_rows]
+  RowParams* h_params;      // host mirror of the uploaded table
+  uint32_t config_rows;     // rows configured by the last set_configs
+  uint64_t* d_cand;         // [max_rows][kMaxChunks][kMaxK]
+  uint64_t* d_greedy;       // [max_rows][kMaxChunks]
+  double* d_lse;            // [max_rows][kMaxChunks][2]
+  uint32_t* d_row_thr;      // [max_rows]
+  uint32_t* d_row_done;     // [max_rows]
+  uint32_t target_groups;   // workgroups per launch the chunking aims for
+};
+
+extern "C" {
+
+fg_status fg_hip_apply_penalties(float* logits, const uint32_t* counts, uint32_t values,
+                                 float presence_penalty, float frequency_penalty,
+                                 float repetition_penalty, void* stream, fg_error* err) {
+  if (!logits || !counts || !values || !isfinite(presence_penalty) ||
+      !isfinite(frequency_penalty) || !isfinite(repetition_penalty) ||
+      repetition_penalty <= 0.0f)
+    return arg_fail(err, "invalid vocabulary penalty dispatch");
+  const uint32_t quads = (values + 3u) / 4u;
+  const uint32_t blocks = (quads + 255u) / 256u;
+  if (aligned16(logits) && aligned16(counts))
+    fg::apply_penalties_kernel<true><<<blocks, 256, 0, as_stream(stream)>>>(
+        logits, counts, values, presence_penalty, frequency_penalty, repetition_penalty);
+  else
+    fg::apply_penalties_kernel<false><<<blocks, 256, 0, as_stream(stream)>>>(
+        logits, counts, values, presence_penalty, frequency_penalty, repetition_penalty);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "penalty launch");
+}
+
+fg_status fg_hip_argmax_reduce(float* output_scores, uint32_t* output_ids,
+                               const float* input_scores, const uint32_t* input_ids,
+                               uint32_t count, uint32_t* output_count, void* stream,
+                               fg_error* err) {
+  if (!output_scores || !output_ids || !input_scores || !count || !output_count)
+    return arg_fail(err, "invalid argmax reduction dispatch");
+  const uint32_t groups = (count + 4095u) / 4096u;
+  fg::argmax_reduce_kernel<<<groups, 256, 0, as_stream(stream)>>>(output_scores, output_ids,
+                                                                   input_scores, input_ids, count);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(err, e, "argmax launch");
+  *output_count = groups;
+  return FG_OK;
+}
+
+fg_status fg_hip_topk_select(float* output_scores, uint32_t* output_ids,
+                             const float* input_scores, const uint32_t* input_ids,
+                             uint32_t count, uint32_t k, uint32_t* output_count, void* stream,
+                             fg_error* err) {
+  const uint32_t groups = (count + 1023u) / 1024u;
+  const uint64_t produced = static_cast<uint64_t>(groups) * k;
+  if (!output_scores || !output_ids || !input_scores || !count || k < 1u || k > 64u ||
+      !output_count || produced > UINT32_MAX)
+    return arg_fail(err, "invalid generation top-k selection dispatch");
+  fg::topk_select_kernel<<<groups, 256, 0, as_stream(stream)>>>(output_scores, output_ids,
+                                                                 input_scores, input_ids, count, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(err, e, "top-k launch");
+  *output_count = static_cast<uint32_t>(produced);
+  return FG_OK;
+}
+
+fg_status fg_hip_history_build(uint32_t* counts, uint64_t counts_stride, uint32_t vocab,
+                               const uint32_t* ids, const uint64_t* offsets, uint32_t rows,
+                               void* stream, fg_error* err) {
+  if (!counts || !vocab || !offsets || !rows || counts_stride < vocab)
+    return arg_fail(err, "invalid output history");
+  hipStream_t s = as_stream(stream);
+  const uint32_t zero = 0u;
+  hipError_t e = hipMemcpyToSymbolAsync(HIP_SYMBOL(g_history_bad), &zero, sizeof zero, 0,
+                                        hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(err, e, "history flag reset");
+  const uint64_t total = static_cast<uint64_t>(rows) * vocab;
+  uint64_t blocks = (total + 255u) / 256u;
+  if (blocks > 65535u * 16u) blocks = 65535u * 16u;
+  fg::fill_u32_kernel<<<static_cast<uint32_t>(blocks), 256, 0, s>>>(counts, counts_stride, vocab,
+                                                                     rows, 0u);
+  uint32_t* bad = nullptr;
+  e = hipGetSymbolAddress(reinterpret_cast<void**>(&bad), HIP_SYMBOL(g_history_bad));
+  if (e != hipSuccess) return hip_fail(err, e, "history flag address");
+  if (ids) {
+    dim3 grid(8, rows);
+    fg::history_count_kernel<<<grid, 256, 0, s>>>(counts, counts_stride, vocab, ids, offsets, bad);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(err, e, "history launch");
+  uint32_t flag = 0u;
+  e = hipMemcpyFromSymbolAsync(&flag, HIP_SYMBOL(g_history_bad), sizeof flag, 0,
+                               hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(err, e, "history check");
+  if (flag) {
+    fg_error_set(err, FG_ERR_FORMAT, "history token is outside vocabulary");
+    return FG_ERR_FORMAT;
+  }
+  return FG_OK;
+}
+
+fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t max_rows,
+                                fg_error* err) {
+  if (!out || !vocab || !max_rows) return arg_fail(err, "invalid sampler dimensions");
+  *out = nullptr;
+  fg_sampler_hip* s = static_cast<fg_sampler_hip*>(calloc(1, sizeof *s));
+  if (!s) {
+    fg_error_set(err, FG_ERR_OOM, "allocate sampler");
+    return FG_ERR_OOM;
+  }
+  s->vocab = vocab;
+  s->max_rows = max_rows;
+  s->target_groups = 2048u;
+  if (const char* t = getenv("FG_HIP_TARGET_GROUPS")) {
+    const long v = strtol(t, nullptr, 10);
+    if (v >= 1 && v <= 1 << 20) s->target_groups = static_cast<uint32_t>(v);
+  }
+  hipError_t e = hipGetDevice(&s->device);
+  const uint64_t slots = static_cast<uint64_t>(max_rows) * fg::kMaxChunks;
+  s->h_params = static_cast<RowParams*>(calloc(max_rows, sizeof(RowParams)));
+  if (!s->h_params) {
+    free(s);
+    fg_error_set(err, FG_ERR_OOM, "allocate sampler");
+    return FG_ERR_OOM;
+  }
+  if (e == hipSuccess) e = hipMalloc(&s->d_params, sizeof(RowParams) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&s->d_cand, sizeof(uint64_t) * slots * fg::kMaxK);
+  if (e == hipSuccess) e = hipMalloc(&s->d_greedy, sizeof(uint64_t) * slots);
+  if (e == hipSuccess) e = hipMalloc(&s->d_lse, sizeof(double) * slots * 2);
+  if (e == hipSuccess) e = hipMalloc(&s->d_row_thr, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&s->d_row_done, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess) e = hipMemset(s->d_row_thr, 0, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess) e = hipMemset(s->d_row_done, 0, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess) e = hipMemset(s->d_params, 0, sizeof(RowParams) * max_rows);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    fg_sampler_hip_destroy(s);
+    return hip_fail(err, e, "sampler workspace");
+  }
+  *out = s;
+  return FG_OK;
+}
+
+void fg_sampler_hip_destroy(fg_sampler_hip* s) {
+  if (!s) return;
+  (void)hipFree(s->d_params);
+  (void)hipFree(s->d_cand);
+  (void)hipFree(s->d_greedy);
+  (void)hipFree(s->d_lse);
+  (void)hipFree(s->d_row_thr);
+  (void)hipFree(s->d_row_done);
+  free(s->h_params);
+  free(s);
+}
+
+fg_status fg_sampler_hip_set_configs(fg_sampler_hip* s, const fg_sampler_config* configs,
+                                     uint32_t rows, uint32_t flags, void* stream, fg_error* err) {
+  if (!s || !configs || !rows || rows > s->max_rows ||
+      (flags & ~FG_SAMPLER_HIP_ALLOW_FULL_VOCAB))
+    return arg_fail(err, "invalid sampler configuration batch");
+  for (uint32_t r = 0; r < rows; r++) {
+    if (!config_ok(&configs[r], flags)) {
+      fg_error_set(err, FG_ERR_ARGUMENT, "invalid sampler controls (row %u)", r);
+      return FG_ERR_ARGUMENT;
+    }
+  }
+  for (uint32_t r = 0; r < rows; r++) {
+    const fg_sampler_config* c = &configs[r];
+    RowParams p{};
+    p.temperature = c->temperature;
+    p.top_p = c->top_p;
+    p.top_k = c->top_k;
+    p.presence = c->presence_penalty;
+    p.frequency = c->frequency_penalty;
+    p.repetition = c->repetition_penalty;
+    p.flags = fg_sampler_penalties_active(c) ? fg::kRowPenalties : 0u;
+    s->h_params[r] = p;
+  }
+  hipError_t e = hipMemcpyAsync(s->d_params, s->h_params, sizeof(RowParams) * rows,
+                                hipMemcpyHostToDevice, as_stream(stream));
+  if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+  if (e != hipSuccess) return hip_fail(err, e, "upload sampler configuration");
+  s->config_rows = rows;
+  return FG_OK;
+}
+
+fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b, void* stream,
+                                fg_error* err) {
+  if (!s || !b) return arg_fail(err, "invalid sampled output arguments");
+  if (!b->logits || !b->tokens || !b->uniforms || !b->rows || b->rows > s->max_rows ||
+      b->rows > s->config_rows || b->logits_stride < s->vocab ||
+      (b->counts && b->counts_stride < s->vocab) || b->logprobs > fg::kMaxK ||
+      (b->logprobs && (!b->logprob_values || !b->logprob_ids)))
+    return arg_fail(err, "invalid sampled output arguments");
+  for (uint32_t r = 0; r < b->rows; r++) {
+    if (s->h_params[r].temperature > 0.0f && s->h_params[r].top_k == 0u) {
+      fg_error_set(err, FG_ERR_UNAVAILABLE, "whole-vocabulary nucleus is not available yet");
+      return FG_ERR_UNAVAILABLE;
+    }
+  }
+  const uint32_t vocab = s->vocab;
+  // Chunking: aim for target_groups workgroups, at most kMaxChunks per row,
+  // each wave slice a multiple of 4 elements.
+  uint32_t chunks = (s->target_groups + b->rows - 1u) / b->rows;
+  if (chunks > fg::kMaxChunks) chunks = fg::kMaxChunks;
+  if (chunks < 1u) chunks = 1u;
+  const uint32_t waves = chunks * fg::kWaves;
+  uint32_t wave_elems = (vocab + waves - 1u) / waves;
+  wave_elems = (wave_elems + 3u) & ~3u;
+  if (wave_elems < 4u) wave_elems = 4u;
+  chunks = (vocab + wave_elems * fg::kWaves - 1u) / (wave_elems * fg::kWaves);
+
+  fg::SampleArgs a{};
+  a.logits = b->logits;
+  a.lstride = b->logits_stride;
+  a.counts = b->counts;
+  a.cstride = b->counts_stride;
+  a.uniforms = b->uniforms;
+  a.params = s->d_params;
+  a.vocab = vocab;
+  a.rows = b->rows;
+  a.chunks = chunks;
+  a.wave_elems = wave_elems;
+  a.logprobs = b->logprobs;
+  a.tokens = b->tokens;
+  a.token_logits = b->token_logits;
+  a.row_status = b->row_status;
+  a.penalised = b->penalised;
+  a.lp_values = b->logprob_values;
+  a.lp_ids = b->logprob_ids;
+  a.cand = s->d_cand;
+  a.greedy = s->d_greedy;
+  a.lse = s->d_lse;
+  a.row_thr = s->d_row_thr;
+  a.row_done = s->d_row_done;
+
+  const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
+                   (!b->counts || (aligned16(b->counts) && (b->counts_stride % 4u) == 0u));
+  const uint32_t grid = b->rows * chunks;
+  if (vec)
+    fg::sample_rows_kernel<true><<<grid, fg::kBlock, 0, as_stream(stream)>>>(a);
+  else
+    fg::sample_rows_kernel<false><<<grid, fg::kBlock, 0, as_stream(stream)>>>(a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "sampler launch");
+}
+
+fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
+                                           uint64_t counts_stride, const uint32_t* tokens,
+                                           const int32_t* row_status, uint32_t rows, void* stream,
+                                           fg_error* err) {
+  if (!s || !counts || !tokens || !rows || rows > s->config_rows || counts_stride < s->vocab)
+    return arg_fail(err, "invalid output history token");
+  fg::history_increment_kernel<<<(rows + 255u) / 256u, 256, 0, as_stream(stream)>>>(
+      counts, counts_stride, s->vocab, tokens, row_status,
+      reinterpret_cast<const uint32_t*>(s->d_params) + offsetof(RowParams, flags) / 4u,
+      sizeof(RowParams) / 4u, rows);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "history increment launch");
+}
+
+}  // extern "C"

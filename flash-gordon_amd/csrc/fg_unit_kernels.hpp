@@ -1,0 +1,195 @@
+// gfx950 kernels behind the unit entry points that stand in for the
+// reference's Vulkan dispatches (src/vk.c:1808-1823, 2237-2260) and its
+// history table upkeep (src/output.c:601-628).
+#pragma once
+
+#include "fg_device.hpp"
+
+namespace fg {
+
+// shaders/fg_apply_penalties.comp, with the C rounding of src/sampler.c:55-58.
+// Each thread owns 4 consecutive logits (one 16-byte access when aligned).
+template <bool kVec>
+__global__ __launch_bounds__(256) void apply_penalties_kernel(float* logits, const uint32_t* counts,
+                                                            uint32_t values, float pres, float freq,
+                                                            float rep) {
+  const uint32_t quads = (values + 3u) / 4u;
+  for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += gridDim.x * blockDim.x) {
+    const uint32_t i = q * 4u;
+    if (kVec && i + 3u < values) {
+      const u4 c = *reinterpret_cast<const u4*>(counts + i);
+      if ((c.x | c.y | c.z | c.w) == 0u) continue;
+      f4 v = *reinterpret_cast<const f4*>(logits + i);
+      v.x = penalise(v.x, c.x, pres, freq, rep);
+      v.y = penalise(v.y, c.y, pres, freq, rep);
+      v.z = penalise(v.z, c.z, pres, freq, rep);
+      v.w = penalise(v.w, c.w, pres, freq, rep);
+      *reinterpret_cast<f4*>(logits + i) = v;
+    } else {
+      for (uint32_t e = 0; e < 4u && i + e < values; e++) {
+        const uint32_t c = counts[i + e];
+        if (c) logits[i + e] = penalise(logits[i + e], c, pres, freq, rep);
+      }
+    }
+  }
+}
+
+// One argmax step over 4096-element slices (shaders/fg_argmax_reduce.comp):
+// greedy composites are max-reduced, the winner's value travels with it.
+__global__ __launch_bounds__(256) void argmax_reduce_kernel(float* out_scores, uint32_t* out_ids,
+                                                          const float* in_scores,
+                                                          const uint32_t* in_ids, uint32_t count) {
+  __shared__ uint64_t s_comp[4];
+  __shared__ float s_val[4];
+  const uint32_t base = blockIdx.x * 4096u;
+  uint64_t best = 0ull;
+  float best_v = -INFINITY;
+  for (uint32_t k = threadIdx.x; k < 4096u; k += 256u) {
+    const uint32_t i = base + k;
+    if (i >= count) break;
+    const float v = in_scores[i];
+    const uint32_t id = in_ids ? in_ids[i] : i;
+    const uint64_t g = greedy_comp(v, id);
+    if (g > best) { best = g; best_v = v; }
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint64_t o = __shfl_xor(best, d);
+    const float ov = __shfl_xor(best_v, d);
+    if (o > best) { best = o; best_v = ov; }
+  }
+  const uint32_t wave = threadIdx.x / kWave;
+  if (lane_id() == 0) { s_comp[wave] = best; s_val[wave] = best_v; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++)
+      if (s_comp[w] > best) { best = s_comp[w]; best_v = s_val[w]; }
+    out_scores[blockIdx.x] = best ? best_v : -INFINITY;
+    out_ids[blockIdx.x] = best ? comp_id(best) : kInvalidId;
+  }
+}
+
+// One top-k step over 1024-element tiles (shaders/fg_topk_select.comp): exact
+// top min(k, tile) finite entries by (key desc, position asc), emitted in tile
+// order, padded with (-inf, invalid).  Thread t owns positions 4t..4t+3.
+__global__ __launch_bounds__(256) void topk_select_kernel(float* out_scores, uint32_t* out_ids,
+                                                        const float* in_scores,
+                                                        const uint32_t* in_ids, uint32_t count,
+                                                        uint32_t k) {
+  __shared__ uint64_t s_buf[1024];
+  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_wave_sel[4];
+  __shared__ uint32_t s_finite;
+  __shared__ uint64_t s_R;
+  const uint32_t t = threadIdx.x;
+  const uint32_t wave = t / kWave;
+  const uint32_t lane = lane_id();
+  const uint32_t base = blockIdx.x * 1024u;
+  const uint32_t avail = min(1024u, count - base);
+  const uint32_t limit = min(k, avail);
+  if (t == 0) s_finite = 0u;
+  __syncthreads();
+  uint64_t comp[4];
+  uint32_t nfin = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const uint32_t pos = 4u * t + e;
+    uint32_t key = 0u;
+    if (pos < avail) key = float_key(in_scores[base + pos]);
+    comp[e] = key ? make_comp(key, pos) : 0ull;
+    s_buf[pos] = comp[e];
+    nfin += key ? 1u : 0u;
+  }
+  atomicAdd(&s_finite, nfin);
+  __syncthreads();
+  const uint32_t take = min(limit, s_finite);
+  if (wave == 0) {
+    uint64_t R = 1ull << 32;  // every finite entry
+    if (take > 0u && take < s_finite) R = wave_select_kth(s_buf, 1024u, take, s_hist);
+    if (lane == 0) s_R = R;
+  }
+  __syncthreads();
+  const uint64_t R = s_R;
+  uint32_t mine = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) mine += (take > 0u && comp[e] >= R && comp[e] >= (1ull << 32)) ? 1u : 0u;
+  // Exclusive prefix of `mine` over the workgroup in thread order.
+  uint32_t incl = mine;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d);
+    if (lane >= static_cast<uint32_t>(d)) incl += o;
+  }
+  if (lane == kWave - 1) s_wave_sel[wave] = incl;
+  __syncthreads();
+  uint32_t off = incl - mine;
+  for (uint32_t w = 0; w < wave; w++) off += s_wave_sel[w];
+  const uint64_t out_base = static_cast<uint64_t>(blockIdx.x) * k;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    if (take > 0u && comp[e] >= R && comp[e] >= (1ull << 32)) {
+      const uint32_t pos = 4u * t + e;
+      out_scores[out_base + off] = in_scores[base + pos];
+      out_ids[out_base + off] = in_ids ? in_ids[base + pos] : base + pos;
+      off++;
+    }
+  }
+  for (uint32_t j = take + t; j < k; j += 256u) {
+    out_scores[out_base + j] = -INFINITY;
+    out_ids[out_base + j] = kInvalidId;
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* dst, uint64_t stride, uint32_t width,
+                                                     uint32_t rows, uint32_t value) {
+  const uint64_t total = static_cast<uint64_t>(rows) * width;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+    const uint64_t r = i / width;
+    dst[r * stride + (i - r * width)] = value;
+  }
+}
+
+__device__ __forceinline__ void saturating_increment(uint32_t* p) {
+  uint32_t old = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (old != 0xffffffffu) {
+    const uint32_t seen = atomicCAS(p, old, old + 1u);
+    if (seen == old) break;
+    old = seen;
+  }
+}
+
+// src/output.c:601-617 for many rows: counts were cleared by fill_u32_kernel.
+// Grid: (blocks per row, rows).  An id >= vocab sets *bad.
+__global__ __launch_bounds__(256) void history_count_kernel(uint32_t* counts, uint64_t stride,
+                                                          uint32_t vocab, const uint32_t* ids,
+                                                          const uint64_t* offsets, uint32_t* bad) {
+  const uint32_t r = blockIdx.y;
+  const uint64_t b = offsets[r], e = offsets[r + 1];
+  for (uint64_t i = b + static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < e;
+       i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+    const uint32_t id = ids[i];
+    if (id >= vocab) {
+      atomicOr(bad, 1u);
+      continue;
+    }
+    saturating_increment(counts + static_cast<uint64_t>(r) * stride + id);
+  }
+}
+
+// src/output.c:752 / :619-628: one saturating increment per sampled row.
+__global__ __launch_bounds__(256) void history_increment_kernel(uint32_t* counts, uint64_t stride,
+                                                              uint32_t vocab, const uint32_t* tokens,
+                                                              const int32_t* status,
+                                                              const uint32_t* row_flags,
+                                                              uint32_t flags_stride, uint32_t rows) {
+  const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  if (!(row_flags[static_cast<uint64_t>(r) * flags_stride] & 1u)) return;
+  if (status && status[r] != 0) return;
+  const uint32_t tok = tokens[r];
+  if (tok >= vocab) return;
+  saturating_increment(counts + static_cast<uint64_t>(r) * stride + tok);
+}
+
+}  // namespace fg

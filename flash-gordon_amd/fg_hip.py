@@ -1,0 +1,235 @@
+"""ctypes binding of lib/libfg_sampler_hip.so (include/fg_sampler.h and
+include/fg_sampler_hip.h).
+
+This is the Python face of the C ABI, used by the tests, smoke() and bench.py.
+Device buffers are passed as torch tensors (their data_ptr()); torch only
+provides device memory and streams.  Every call goes to the HIP library; there
+is no fallback, and a missing library raises at load time.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "lib" / "libfg_sampler_hip.so"
+
+FG_OK = 0
+FG_ERR_ARGUMENT = 2
+FG_ERR_IO = 3
+FG_ERR_FORMAT = 4
+FG_ERR_MISMATCH = 5
+FG_ERR_OOM = 6
+FG_ERR_UNAVAILABLE = 7
+FG_ERR_LIMIT = 8
+FG_ERR_INTERRUPTED = 9
+
+INVALID_ID = 0xFFFFFFFF
+MAX_TOPK = 64
+ALLOW_FULL_VOCAB = 1
+
+# Every symbol include/*.h declares (checked by tests/test_abi.py).
+EXPORTS = (
+    "fg_error_set",
+    "fg_sampler_config_greedy", "fg_sampler_config_defaults", "fg_sampler_config_validate",
+    "fg_sampler_state_init", "fg_sampler_uniform", "fg_sampler_select",
+    "fg_sampler_penalties_active", "fg_sampler_apply_penalties",
+    "fg_hip_apply_penalties", "fg_hip_argmax_reduce", "fg_hip_topk_select",
+    "fg_hip_history_build",
+    "fg_sampler_hip_create", "fg_sampler_hip_destroy", "fg_sampler_hip_set_configs",
+    "fg_sampler_hip_sample", "fg_sampler_hip_history_increment",
+)
+
+
+class FgError(C.Structure):
+    _fields_ = [("code", C.c_int), ("message", C.c_char * 512)]
+
+
+class SamplerConfig(C.Structure):
+    """fg_sampler_config (include/fg_sampler.h)."""
+    _fields_ = [
+        ("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_uint32),
+        ("presence_penalty", C.c_float), ("frequency_penalty", C.c_float),
+        ("repetition_penalty", C.c_float), ("min_p", C.c_float), ("seed", C.c_uint64),
+    ]
+
+
+class SamplerState(C.Structure):
+    _fields_ = [("state", C.c_uint64)]
+
+
+class Batch(C.Structure):
+    """fg_sampler_hip_batch (include/fg_sampler_hip.h)."""
+    _fields_ = [
+        ("logits", C.c_void_p), ("logits_stride", C.c_uint64),
+        ("counts", C.c_void_p), ("counts_stride", C.c_uint64),
+        ("uniforms", C.c_void_p), ("rows", C.c_uint32),
+        ("tokens", C.c_void_p), ("token_logits", C.c_void_p), ("row_status", C.c_void_p),
+        ("penalised", C.c_void_p), ("logprobs", C.c_uint32),
+        ("logprob_values", C.c_void_p), ("logprob_ids", C.c_void_p),
+    ]
+
+
+class FgStatusError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"fg_status {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+def load_library(path: Path | str | None = None) -> C.CDLL:
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"HIP sampling library not built: {p} is missing (run __graft_entry__.build())")
+    lib = C.CDLL(str(p))
+    P = C.c_void_p
+    E = C.POINTER(FgError)
+    u32, u64, f32 = C.c_uint32, C.c_uint64, C.c_float
+    sig = {
+        "fg_sampler_config_greedy": (None, [C.POINTER(SamplerConfig)]),
+        "fg_sampler_config_defaults": (None, [C.POINTER(SamplerConfig)]),
+        "fg_sampler_config_validate": (C.c_int, [C.POINTER(SamplerConfig), E]),
+        "fg_sampler_state_init": (None, [C.POINTER(SamplerState), u64]),
+        "fg_sampler_uniform": (f32, [C.POINTER(SamplerState)]),
+        "fg_sampler_select": (C.c_int, [C.POINTER(SamplerConfig), P, P, u32, f32, P, P, E]),
+        "fg_sampler_penalties_active": (C.c_bool, [C.POINTER(SamplerConfig)]),
+        "fg_sampler_apply_penalties": (None, [P, P, P, u32, C.POINTER(SamplerConfig)]),
+        "fg_hip_apply_penalties": (C.c_int, [P, P, u32, f32, f32, f32, P, E]),
+        "fg_hip_argmax_reduce": (C.c_int, [P, P, P, P, u32, C.POINTER(u32), P, E]),
+        "fg_hip_topk_select": (C.c_int, [P, P, P, P, u32, u32, C.POINTER(u32), P, E]),
+        "fg_hip_history_build": (C.c_int, [P, u64, u32, P, P, u32, P, E]),
+        "fg_sampler_hip_create": (C.c_int, [C.POINTER(P), u32, u32, E]),
+        "fg_sampler_hip_destroy": (None, [P]),
+        "fg_sampler_hip_set_configs": (C.c_int, [P, C.POINTER(SamplerConfig), u32, u32, P, E]),
+        "fg_sampler_hip_sample": (C.c_int, [P, C.POINTER(Batch), P, E]),
+        "fg_sampler_hip_history_increment": (C.c_int, [P, P, u64, P, P, u32, P, E]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_LIB: C.CDLL | None = None
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        _LIB = load_library()
+    return _LIB
+
+
+def _check(status: int, err: FgError) -> None:
+    if status != FG_OK:
+        raise FgStatusError(status, err.message.decode(errors="replace"))
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return int(stream)
+
+
+def make_config(temperature=1.0, top_p=0.95, top_k=20, presence=0.0, frequency=0.0,
+                repetition=1.0, min_p=0.0, seed=0x9E3779B97F4A7C15) -> SamplerConfig:
+    return SamplerConfig(temperature, top_p, top_k, presence, frequency, repetition, min_p, seed)
+
+
+# ---- unit kernels ----------------------------------------------------------
+
+def apply_penalties(logits, counts, presence, frequency, repetition, stream=None):
+    err = FgError()
+    _check(lib().fg_hip_apply_penalties(_ptr(logits), _ptr(counts), logits.numel(),
+                                        presence, frequency, repetition, _stream(stream),
+                                        C.byref(err)), err)
+
+
+def argmax_reduce(out_scores, out_ids, in_scores, in_ids, count, stream=None) -> int:
+    err = FgError()
+    n = C.c_uint32(0)
+    _check(lib().fg_hip_argmax_reduce(_ptr(out_scores), _ptr(out_ids), _ptr(in_scores),
+                                      _ptr(in_ids), count, C.byref(n), _stream(stream),
+                                      C.byref(err)), err)
+    return n.value
+
+
+def topk_select(out_scores, out_ids, in_scores, in_ids, count, k, stream=None) -> int:
+    err = FgError()
+    n = C.c_uint32(0)
+    _check(lib().fg_hip_topk_select(_ptr(out_scores), _ptr(out_ids), _ptr(in_scores),
+                                    _ptr(in_ids), count, k, C.byref(n), _stream(stream),
+                                    C.byref(err)), err)
+    return n.value
+
+
+def history_build(counts, stride, vocab, ids, offsets, rows, stream=None):
+    err = FgError()
+    _check(lib().fg_hip_history_build(_ptr(counts), stride, vocab, _ptr(ids), _ptr(offsets),
+                                      rows, _stream(stream), C.byref(err)), err)
+
+
+# ---- batched sampler -------------------------------------------------------
+
+class HipSampler:
+    """Owns an fg_sampler_hip context (device workspace for max_rows rows)."""
+
+    def __init__(self, vocab: int, max_rows: int):
+        self._lib = lib()
+        err = FgError()
+        h = C.c_void_p()
+        _check(self._lib.fg_sampler_hip_create(C.byref(h), vocab, max_rows, C.byref(err)), err)
+        self.handle = h
+        self.vocab = vocab
+        self.max_rows = max_rows
+
+    def close(self):
+        if self.handle:
+            self._lib.fg_sampler_hip_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_configs(self, configs, flags=0, stream=None):
+        arr = (SamplerConfig * len(configs))(*configs)
+        err = FgError()
+        _check(self._lib.fg_sampler_hip_set_configs(self.handle, arr, len(configs), flags,
+                                                    _stream(stream), C.byref(err)), err)
+
+    def sample(self, logits, uniforms, tokens, counts=None, token_logits=None, row_status=None,
+               penalised=None, logprobs=0, logprob_values=None, logprob_ids=None, rows=None,
+               logits_stride=None, counts_stride=None, stream=None):
+        rows = rows if rows is not None else logits.shape[0]
+        b = Batch(
+            _ptr(logits), logits_stride if logits_stride is not None else logits.stride(0),
+            _ptr(counts), (counts_stride if counts_stride is not None
+                           else (counts.stride(0) if counts is not None else 0)),
+            _ptr(uniforms), rows, _ptr(tokens), _ptr(token_logits), _ptr(row_status),
+            _ptr(penalised), logprobs, _ptr(logprob_values), _ptr(logprob_ids))
+        err = FgError()
+        _check(self._lib.fg_sampler_hip_sample(self.handle, C.byref(b), _stream(stream),
+                                               C.byref(err)), err)
+
+    def history_increment(self, counts, tokens, row_status=None, rows=None, stream=None):
+        rows = rows if rows is not None else tokens.numel()
+        err = FgError()
+        _check(self._lib.fg_sampler_hip_history_increment(
+            self.handle, _ptr(counts), counts.stride(0), _ptr(tokens), _ptr(row_status), rows,
+            _stream(stream), C.byref(err)), err)
+
+
+def env_summary() -> dict:
+    return {"lib": str(LIB_PATH), "exists": LIB_PATH.exists(),
+            "target_groups": os.environ.get("FG_HIP_TARGET_GROUPS")}

@@ -1,0 +1,158 @@
+/* MI355X (gfx950) token-sampling path: the C ABI.
+ *
+ * Plain C, plain pointers and sizes.  Every device pointer below is a HIP
+ * device address owned by the caller; `stream` is a hipStream_t passed as
+ * void* (NULL = the null stream).  All launches are stream-ordered and return
+ * without synchronising.  Invalid arguments return FG_ERR_ARGUMENT with a
+ * message and launch nothing, as the reference's Vulkan wrappers do
+ * (src/vk.c:1812-1818, 2240-2248, 2260).  No C++ exception crosses this ABI.
+ *
+ * Two layers are exported:
+ *
+ *  1. Unit kernels that replace the reference's three GPU entry points one for
+ *     one (same arguments, same output counts, same error behaviour), so a
+ *     port of src/output.c:681-756 can swap the Vulkan ladder for HIP:
+ *        fg_hip_apply_penalties   <- fg_vk_apply_penalties  include/fg_vk.h:324-327
+ *        fg_hip_argmax_reduce     <- fg_vk_argmax_reduce    include/fg_vk.h:509-512
+ *        fg_hip_topk_select       <- fg_vk_topk_select      include/fg_vk.h:494-499
+ *
+ *  2. The batched sampler, which replaces the per-row orchestration of
+ *     fg_output_sample (src/output.c:702-756: penalties -> argmax | top-k ->
+ *     readback -> fg_sampler_select -> history increment) with one fused
+ *     launch over many rows that ends in a token id per row on the device.
+ */
+#ifndef FLASH_GORDON_SAMPLER_HIP_H
+#define FLASH_GORDON_SAMPLER_HIP_H
+
+#include "fg_sampler.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Padding id written by top-k / argmax for slots with no finite candidate
+ * (shaders/fg_topk_select.comp:16, fg_argmax_reduce.comp:15). */
+#define FG_HIP_INVALID_ID 0xffffffffu
+/* Largest top_k and largest log-prob count per row (src/sampler.c:27). */
+#define FG_HIP_MAX_TOPK 64u
+
+/* ------------------------------------------------------------------------ */
+/* 1. Unit kernels                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* In-place penalties over `values` logits from a dense u32 count table of the
+ * same length (identity token ids).  Replaces fg_vk_apply_penalties
+ * (src/vk.c:1808-1823, shaders/fg_apply_penalties.comp).  Rounds as the C
+ * formula of src/sampler.c:55-58: s' = rep(s) - (freq*(float)c + pres).
+ * Errors: values == 0, NULL pointers, non-finite penalty, repetition <= 0. */
+fg_status fg_hip_apply_penalties(float *logits, const uint32_t *counts, uint32_t values,
+                                 float presence_penalty, float frequency_penalty,
+                                 float repetition_penalty, void *stream, fg_error *err);
+
+/* One argmax step: the best (value, id) of each 4096-element slice is written
+ * to out_*[slice]; *output_count = ceil(count / 4096).  Call repeatedly until
+ * one remains (src/output.c:565, 728-733).  Order: real ids before padding,
+ * non-finite before finite (lower id first), then larger value, then lower id
+ * (shaders/fg_argmax_reduce.comp:14-24).  in_ids == NULL means ids 0..count-1.
+ * Replaces fg_vk_argmax_reduce (src/vk.c:2260). */
+fg_status fg_hip_argmax_reduce(float *output_scores, uint32_t *output_ids,
+                               const float *input_scores, const uint32_t *input_ids,
+                               uint32_t count, uint32_t *output_count,
+                               void *stream, fg_error *err);
+
+/* One top-k step: each 1024-element tile yields its exact top min(k, tile)
+ * finite candidates by the order-preserving float key (NaN/Inf excluded,
+ * +0 above -0, lower position first on ties), padded with (-inf,
+ * FG_HIP_INVALID_ID); *output_count = ceil(count/1024) * k.  Call repeatedly
+ * until output_count <= k (src/output.c:681-700).  The reference leaves the
+ * order inside a tile unspecified (include/fg_vk.h:492-493); here the
+ * selected entries keep their tile order, so equal keys stay in position
+ * order and the ladder's fixed point is the exact top-k by (key desc, id
+ * asc).  in_ids == NULL means ids 0..count-1.  Errors: k outside [1, 64],
+ * count == 0.  Replaces fg_vk_topk_select (src/vk.c:2237-2258). */
+fg_status fg_hip_topk_select(float *output_scores, uint32_t *output_ids,
+                             const float *input_scores, const uint32_t *input_ids,
+                             uint32_t count, uint32_t k, uint32_t *output_count,
+                             void *stream, fg_error *err);
+
+/* Dense history count tables from token lists: for each row r, counts[r*stride
+ * .. +vocab) is cleared and then incremented once per id in
+ * ids[offsets[r] .. offsets[r+1]), saturating at UINT32_MAX.  Replaces
+ * fg_output_history_reset (src/output.c:601-617) for many rows at once.
+ * An id >= vocab makes the call fail with FG_ERR_FORMAT after a device check
+ * (this entry point synchronises `stream` to report it). */
+fg_status fg_hip_history_build(uint32_t *counts, uint64_t counts_stride, uint32_t vocab,
+                               const uint32_t *ids, const uint64_t *offsets,
+                               uint32_t rows, void *stream, fg_error *err);
+
+/* ------------------------------------------------------------------------ */
+/* 2. Batched sampler                                                        */
+/* ------------------------------------------------------------------------ */
+
+typedef struct fg_sampler_hip fg_sampler_hip;
+
+/* Extension flag for fg_sampler_hip_set_configs: accept top_k == 0, meaning
+ * "no top-k" (nucleus over the whole vocabulary).  The reference rejects
+ * top_k == 0 (src/sampler.c:27); without this flag so does this library. */
+#define FG_SAMPLER_HIP_ALLOW_FULL_VOCAB 1u
+
+/* Creates a sampler for rows of `vocab` logits and up to `max_rows` rows per
+ * call.  Allocates the device workspace once (candidate lists, row counters);
+ * the calls below allocate nothing.  Uses the current HIP device. */
+fg_status fg_sampler_hip_create(fg_sampler_hip **out, uint32_t vocab, uint32_t max_rows,
+                                fg_error *err);
+void fg_sampler_hip_destroy(fg_sampler_hip *sampler);
+
+/* Validates each row's controls as fg_sampler_config_validate does and copies
+ * them to the device table used by later fg_sampler_hip_sample calls
+ * (stream-ordered).  Row r of a batch uses configs[r]. */
+fg_status fg_sampler_hip_set_configs(fg_sampler_hip *sampler, const fg_sampler_config *configs,
+                                     uint32_t rows, uint32_t flags, void *stream,
+                                     fg_error *err);
+
+typedef struct fg_sampler_hip_batch {
+    const float *logits;        /* rows x logits_stride f32, read only */
+    uint64_t logits_stride;     /* elements between rows, >= vocab */
+    const uint32_t *counts;     /* rows x counts_stride u32 history counts, or NULL */
+    uint64_t counts_stride;     /* elements between rows, >= vocab */
+    const float *uniforms;      /* one uniform per row (unused by greedy rows) */
+    uint32_t rows;              /* 1 .. max_rows */
+    uint32_t *tokens;           /* out: chosen id per row */
+    float *token_logits;        /* out (optional): penalised, untempered logit of the id */
+    int32_t *row_status;        /* out (optional): fg_status per row */
+    float *penalised;           /* out (optional): rows x vocab penalised logits */
+    uint32_t logprobs;          /* 0 .. 64 top log-probs per row */
+    float *logprob_values;      /* out: rows x logprobs, s/T - logsumexp(s/T) */
+    uint32_t *logprob_ids;      /* out: rows x logprobs */
+} fg_sampler_hip_batch;
+
+/* Samples one token per row in one launch.  Per row, with the row's config:
+ *   penalties (when fg_sampler_penalties_active and counts != NULL),
+ *   T == 0: argmax with the reference's greedy order; a non-finite winner sets
+ *           row_status FG_ERR_MISMATCH (no penalties, src/output.c:593) or
+ *           FG_ERR_FORMAT (penalties, src/output.c:736-740);
+ *   T  > 0: exact top_k by float key, then fg_sampler_select's arithmetic on
+ *           those candidates with the row's uniform (src/sampler.c:80-122);
+ *           top_k == 0 (extension) runs the same rule over the whole row.
+ * Log-probs: the first `logprobs` of the row's max(top_k, logprobs) best
+ * candidates ordered by (value desc, id asc), lp = s/T - logsumexp_j(s_j/T)
+ * over the finite penalised logits of the row (T == 0 uses T = 1).
+ * Rows are independent.  One call at a time per sampler: calls on different
+ * streams that overlap on one sampler race on its workspace. */
+fg_status fg_sampler_hip_sample(fg_sampler_hip *sampler, const fg_sampler_hip_batch *batch,
+                                void *stream, fg_error *err);
+
+/* After a draw, adds 1 (saturating) to counts[r*stride + tokens[r]] for every
+ * row whose config has penalties active and whose row_status is FG_OK (or
+ * row_status == NULL).  Replaces fg_output_history_increment as called at
+ * src/output.c:752. */
+fg_status fg_sampler_hip_history_increment(fg_sampler_hip *sampler, uint32_t *counts,
+                                           uint64_t counts_stride, const uint32_t *tokens,
+                                           const int32_t *row_status, uint32_t rows,
+                                           void *stream, fg_error *err);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

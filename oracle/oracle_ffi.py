@@ -1,0 +1,230 @@
+"""ctypes binding of the CPU oracle (oracle/_build/libfg_oracle.so) and of the
+reference's own sampler built from its sources (oracle/_ref/libfg_ref_sampler.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker and the timed CPU baseline.  The
+product library never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_LIB = HERE / "_build" / "libfg_oracle.so"
+REF_LIB = HERE / "_ref" / "libfg_ref_sampler.so"
+REF_TEST = HERE / "_ref" / "test_sampler_ref"
+INVALID_ID = 0xFFFFFFFF
+
+
+class Config(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_uint32),
+                ("presence", C.c_float), ("frequency", C.c_float), ("repetition", C.c_float)]
+
+
+class Result(C.Structure):
+    _fields_ = [("token", C.c_uint32), ("logit", C.c_float), ("status", C.c_int32),
+                ("cutoff", C.c_uint32), ("margin", C.c_double)]
+
+
+class RefConfig(C.Structure):
+    """fg_sampler_config layout, for the reference library."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_uint32),
+                ("presence_penalty", C.c_float), ("frequency_penalty", C.c_float),
+                ("repetition_penalty", C.c_float), ("min_p", C.c_float), ("seed", C.c_uint64)]
+
+
+class RefError(C.Structure):
+    _fields_ = [("code", C.c_int), ("message", C.c_char * 512)]
+
+
+_O = None
+_R = None
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+def oracle() -> C.CDLL:
+    global _O
+    if _O is None:
+        if not ORACLE_LIB.exists():
+            raise RuntimeError(f"oracle not built: {ORACLE_LIB}")
+        o = C.CDLL(str(ORACLE_LIB))
+        P, u32, u64, f32, f64 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_float, C.c_double
+        sig = {
+            "fgo_philox4x32_10": (None, [P, P, P]),
+            "fgo_xorshift_uniform": (f32, [C.POINTER(u64)]),
+            "fgo_float_key": (u32, [f32]),
+            "fgo_penalties_c": (None, [P, P, u32, f32, f32, f32]),
+            "fgo_penalties_glsl": (None, [P, P, u32, f32, f32, f32]),
+            "fgo_greedy_before": (C.c_int, [f32, u32, f32, u32]),
+            "fgo_argmax_reduce_step": (u32, [P, P, P, P, u32]),
+            "fgo_topk_select_step": (u32, [P, P, P, P, u32, u32]),
+            "fgo_topk_row": (u32, [P, u32, u32, P, P]),
+            "fgo_select": (C.c_int32, [f32, f32, u32, P, P, u32, f32, P, P, P, P]),
+            "fgo_sample_rows": (C.c_int, [P, P, u64, P, u64, u32, P, u32, u32, P, P, P, P, u32]),
+            "fgo_u01": (f64, [u32]),
+            "fgo_gen_uniforms": (None, [P, u32, u32, u32]),
+            "fgo_gen_logits": (None, [P, u64, u32, u32, C.c_int, f64, f64, f64, u32, u32]),
+            "fgo_gen_zipf_ids": (None, [P, u32, u32, u32, f64, u32, u32]),
+            "fgo_gen_uniform_ids": (None, [P, u32, u32, u32, u32, u32]),
+            "fgo_build_counts": (None, [P, u64, u32, u32, P, u32]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(o, name)
+            fn.restype = res
+            fn.argtypes = args
+        _O = o
+    return _O
+
+
+def reference_available() -> bool:
+    return REF_LIB.exists()
+
+
+def reference() -> C.CDLL:
+    global _R
+    if _R is None:
+        r = C.CDLL(str(REF_LIB))
+        P, u32, f32 = C.c_void_p, C.c_uint32, C.c_float
+        r.fg_sampler_select.restype = C.c_int
+        r.fg_sampler_select.argtypes = [C.POINTER(RefConfig), P, P, u32, f32, P, P,
+                                        C.POINTER(RefError)]
+        r.fg_sampler_apply_penalties.restype = None
+        r.fg_sampler_apply_penalties.argtypes = [P, P, P, u32, C.POINTER(RefConfig)]
+        r.fg_sampler_uniform.restype = f32
+        r.fg_sampler_uniform.argtypes = [P]
+        r.fg_sampler_state_init.restype = None
+        r.fg_sampler_state_init.argtypes = [P, C.c_uint64]
+        r.fg_sampler_config_validate.restype = C.c_int
+        r.fg_sampler_config_validate.argtypes = [C.POINTER(RefConfig), C.POINTER(RefError)]
+        _R = r
+    return _R
+
+
+# ---- numpy helpers -----------------------------------------------------------
+
+def philox(ctr, key):
+    c = np.asarray(ctr, dtype=np.uint32)
+    k = np.asarray(key, dtype=np.uint32)
+    out = np.zeros(4, dtype=np.uint32)
+    oracle().fgo_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def gen_logits(rows, n, kind, sigma, sigma2=0.0, nu=0.0, seed=1, config_id=0):
+    out = np.zeros((rows, n), dtype=np.float32)
+    oracle().fgo_gen_logits(_p(out), n, rows, n, kind, sigma, sigma2, nu, seed, config_id)
+    return out
+
+
+def gen_uniforms(rows, seed, config_id):
+    out = np.zeros(rows, dtype=np.float32)
+    oracle().fgo_gen_uniforms(_p(out), rows, seed, config_id)
+    return out
+
+
+def gen_zipf_ids(rows, per_row, n, s, seed, config_id):
+    out = np.zeros((rows, per_row), dtype=np.uint32)
+    oracle().fgo_gen_zipf_ids(_p(out), rows, per_row, n, s, seed, config_id)
+    return out
+
+
+def gen_uniform_ids(rows, per_row, n, seed, config_id):
+    out = np.zeros((rows, per_row), dtype=np.uint32)
+    oracle().fgo_gen_uniform_ids(_p(out), rows, per_row, n, seed, config_id)
+    return out
+
+
+def build_counts(ids, n):
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    rows, per_row = ids.shape
+    out = np.zeros((rows, n), dtype=np.uint32)
+    oracle().fgo_build_counts(_p(out), n, rows, n, _p(ids), per_row)
+    return out
+
+
+def penalties_c(scores, counts, presence, frequency, repetition):
+    s = np.ascontiguousarray(scores, dtype=np.float32).copy()
+    c = np.ascontiguousarray(counts, dtype=np.uint32)
+    oracle().fgo_penalties_c(_p(s), _p(c), s.size, presence, frequency, repetition)
+    return s
+
+
+def penalties_glsl(scores, counts, presence, frequency, repetition):
+    s = np.ascontiguousarray(scores, dtype=np.float32).copy()
+    c = np.ascontiguousarray(counts, dtype=np.uint32)
+    oracle().fgo_penalties_glsl(_p(s), _p(c), s.size, presence, frequency, repetition)
+    return s
+
+
+def argmax_reduce_step(scores, ids=None):
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    i = None if ids is None else np.ascontiguousarray(ids, dtype=np.uint32)
+    groups = (s.size + 4095) // 4096
+    os_ = np.zeros(groups, dtype=np.float32)
+    oi = np.zeros(groups, dtype=np.uint32)
+    oracle().fgo_argmax_reduce_step(_p(os_), _p(oi), _p(s), _p(i), s.size)
+    return os_, oi
+
+
+def topk_select_step(scores, k, ids=None):
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    i = None if ids is None else np.ascontiguousarray(ids, dtype=np.uint32)
+    tiles = (s.size + 1023) // 1024
+    os_ = np.zeros(tiles * k, dtype=np.float32)
+    oi = np.zeros(tiles * k, dtype=np.uint32)
+    oracle().fgo_topk_select_step(_p(os_), _p(oi), _p(s), _p(i), s.size, k)
+    return os_, oi
+
+
+def topk_row(scores, k):
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    os_ = np.zeros(k, dtype=np.float32)
+    oi = np.zeros(k, dtype=np.uint32)
+    have = oracle().fgo_topk_row(_p(s), s.size, k, _p(os_), _p(oi))
+    return os_, oi, have
+
+
+def select(temperature, top_p, top_k, scores, ids, uniform):
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    i = np.ascontiguousarray(ids, dtype=np.uint32)
+    tok, logit, cut, margin = C.c_uint32(), C.c_float(), C.c_uint32(), C.c_double()
+    st = oracle().fgo_select(temperature, top_p, top_k, _p(s), _p(i), s.size, uniform,
+                             C.byref(tok), C.byref(logit), C.byref(cut), C.byref(margin))
+    return st, tok.value, logit.value, cut.value, margin.value
+
+
+def sample_rows(configs, logits, uniforms, counts=None, logprobs=0, want_penalised=False,
+                threads=1):
+    """configs: list of dicts with temperature/top_p/top_k/presence/frequency/repetition."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, n = logits.shape
+    cfg = (Config * rows)(*[Config(c["temperature"], c["top_p"], c["top_k"], c.get("presence", 0.0),
+                                   c.get("frequency", 0.0), c.get("repetition", 1.0))
+                            for c in configs])
+    res = (Result * rows)()
+    u = np.ascontiguousarray(uniforms, dtype=np.float32)
+    cnt = None if counts is None else np.ascontiguousarray(counts, dtype=np.uint32)
+    lpv = np.zeros((rows, max(logprobs, 1)), dtype=np.float32)
+    lpi = np.zeros((rows, max(logprobs, 1)), dtype=np.uint32)
+    pen = np.zeros((rows, n), dtype=np.float32) if want_penalised else None
+    oracle().fgo_sample_rows(cfg, _p(logits), n, _p(cnt), n if cnt is not None else 0, n,
+                             _p(u), rows, logprobs, res, _p(lpv), _p(lpi), _p(pen), threads)
+    out = {
+        "token": np.array([r.token for r in res], dtype=np.uint32),
+        "logit": np.array([r.logit for r in res], dtype=np.float32),
+        "status": np.array([r.status for r in res], dtype=np.int32),
+        "cutoff": np.array([r.cutoff for r in res], dtype=np.uint32),
+        "margin": np.array([r.margin for r in res], dtype=np.float64),
+    }
+    if logprobs:
+        out["lp_values"] = lpv[:, :logprobs]
+        out["lp_ids"] = lpi[:, :logprobs]
+    if want_penalised:
+        out["penalised"] = pen
+    return out

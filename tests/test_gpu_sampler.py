@@ -1,0 +1,232 @@
+"""GPU parity: the HIP batched sampler (C ABI fg_sampler_hip_sample) against the
+CPU oracle on identical inputs and identical per-row uniforms.
+
+Bar: token ids bit-exact, except where the oracle's
+f64 running sums come within 1e-6 (relative) of a top-p or draw boundary;
+penalised logits within 1e-6 relative (the C rounding is reproduced exactly, so
+the check is bit-exact); log-probs within 1e-5 absolute.
+"""
+import numpy as np
+import pytest
+
+import fg_hip
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+BOUNDARY = 1e-6
+LP_TOL = 1e-5
+
+
+def to_dev(a, dev):
+    import torch
+    if a.dtype == np.uint32:
+        return torch.from_numpy(a.view(np.int32)).to(dev)
+    return torch.from_numpy(a).to(dev)
+
+
+def run_hip(w, dev, logprobs=None, penalised=False, flags=0, sampler=None, counts=True):
+    import torch
+    logits = w["logits"]
+    rows, vocab = logits.shape
+    L = w["logprobs"] if logprobs is None else logprobs
+    s = sampler or fg_hip.HipSampler(vocab, rows)
+    s.set_configs([fg_hip.make_config(c["temperature"], c["top_p"], c["top_k"], c["presence"],
+                                      c["frequency"], c["repetition"]) for c in w["configs"]],
+                  flags=flags)
+    d_logits = to_dev(logits, dev)
+    d_counts = to_dev(w["counts"], dev) if counts else None
+    d_u = to_dev(w["uniforms"], dev)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    tl = torch.empty(rows, dtype=torch.float32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    pen = torch.empty((rows, vocab), dtype=torch.float32, device=dev) if penalised else None
+    lpv = torch.empty((rows, max(L, 1)), dtype=torch.float32, device=dev)
+    lpi = torch.empty((rows, max(L, 1)), dtype=torch.int32, device=dev)
+    s.sample(d_logits, d_u, tok, counts=d_counts, token_logits=tl, row_status=st, penalised=pen,
+             logprobs=L, logprob_values=lpv if L else None, logprob_ids=lpi if L else None)
+    torch.cuda.synchronize()
+    out = dict(token=tok.cpu().numpy().view(np.uint32), logit=tl.cpu().numpy(),
+               status=st.cpu().numpy())
+    if penalised:
+        out["penalised"] = pen.cpu().numpy()
+    if L:
+        out["lp_values"] = lpv.cpu().numpy()[:, :L]
+        out["lp_ids"] = lpi.cpu().numpy().view(np.uint32)[:, :L]
+    return out
+
+
+def check(w, got, ref, name):
+    st_ok = np.array_equal(got["status"], ref["status"])
+    assert st_ok, f"{name}: status {got['status']} vs {ref['status']}"
+    ok = ref["status"] == 0
+    same = got["token"] == ref["token"]
+    near = ref["margin"] < BOUNDARY
+    bad = ok & ~same & ~near
+    assert not bad.any(), (
+        f"{name}: rows {np.nonzero(bad)[0][:10]} token {got['token'][bad][:10]} "
+        f"vs oracle {ref['token'][bad][:10]} (margin {ref['margin'][bad][:10]})")
+    exact = ok & same
+    assert np.array_equal(got["logit"][exact].view(np.uint32), ref["logit"][exact].view(np.uint32)), \
+        f"{name}: token logits differ"
+    if "lp_values" in ref:
+        assert np.array_equal(got["lp_ids"], ref["lp_ids"]), f"{name}: log-prob ids differ"
+        fin = np.isfinite(ref["lp_values"])
+        assert np.array_equal(fin, np.isfinite(got["lp_values"]))
+        err = np.abs(got["lp_values"][fin].astype(np.float64) - ref["lp_values"][fin])
+        assert err.max(initial=0.0) <= LP_TOL, f"{name}: log-prob error {err.max()}"
+    return int(near.sum())
+
+
+def test_config1_greedy_repetition(dev):
+    w = W.config1()
+    check(w, run_hip(w, dev), W.oracle_run(w), "config1")
+
+
+def test_config2_north_star(dev):
+    w = W.config2()
+    got = run_hip(w, dev, penalised=True)
+    ref = W.oracle_run(w, want_penalised=True)
+    check(w, got, ref, "config2")
+    assert np.array_equal(got["penalised"].view(np.uint32), ref["penalised"].view(np.uint32))
+
+
+def test_config2_repeated_launches(dev):
+    """The row counters and thresholds reset themselves: three launches in a row
+    on one sampler, the middle one with fewer rows, all match."""
+    w = W.config2(rows=48)
+    s = fg_hip.HipSampler(W.V, 48)
+    ref = W.oracle_run(w)
+    check(w, run_hip(w, dev, sampler=s), ref, "launch 1")
+    small = {k: (v[:17] if k in ("logits", "counts", "uniforms", "configs") else v)
+             for k, v in w.items()}
+    check(small, run_hip(small, dev, sampler=s), W.oracle_run(small), "launch 2")
+    check(w, run_hip(w, dev, sampler=s), ref, "launch 3")
+
+
+@pytest.mark.parametrize("sampled", [False, True])
+def test_config4_ties(dev, sampled):
+    w = W.config4(sampled=sampled)
+    check(w, run_hip(w, dev), W.oracle_run(w), f"config4 sampled={sampled}")
+
+
+def test_config5_logprobs(dev):
+    w = W.config5(rows=64)
+    check(w, run_hip(w, dev), W.oracle_run(w), "config5")
+
+
+def test_mixed_rows_and_greedy_logprobs(dev):
+    """Greedy, sampled and unpenalised rows in one batch, with log-probs."""
+    w = W.config2(rows=12)
+    for r in range(0, 12, 3):
+        w["configs"][r] = W.cfg(0.0, 1.0, 1, presence=0.5 if r % 2 else 0.0)
+    w["configs"][4] = W.cfg(1.3, 0.5, 64)
+    w["configs"][5] = W.cfg(0.2, 1.0, 1)
+    w["logprobs"] = 8
+    check(w, run_hip(w, dev), W.oracle_run(w), "mixed")
+
+
+@pytest.mark.parametrize("vocab", [1, 3, 5, 63, 64, 1000, 1001, 4097, 65537])
+def test_small_and_ragged_vocab(dev, vocab):
+    w = W.config2(rows=5, vocab=vocab)
+    w["configs"][0] = W.cfg(0.0, 1.0, 1)
+    w["logprobs"] = 4
+    check(w, run_hip(w, dev), W.oracle_run(w), f"vocab {vocab}")
+
+
+def test_non_finite_and_ties(dev):
+    rng = np.random.default_rng(7)
+    vocab = 20_000
+    rows = 10
+    logits = rng.normal(0, 2, (rows, vocab)).astype(np.float32)
+    logits[0, 777] = np.nan                      # greedy: non-finite wins -> error
+    logits[1, :] = 1.5                           # all equal: lowest ids win
+    logits[2, ::2] = np.inf                      # half +inf: excluded by top-k
+    logits[3, :] = np.nan
+    logits[3, [5, 900, 19_999]] = [1.0, 2.0, 2.0]  # only 3 finite, k=20
+    logits[4, :] = 0.0
+    logits[4, ::3] = -0.0                        # +0 ranks above -0 in the key order
+    logits[5, :] = np.nan                        # no finite candidate -> error
+    logits[6, 100] = np.float32(3e38)            # large values
+    logits[6, 101] = np.float32(3e38)
+    logits[7, :] = -np.inf
+    logits[7, 42] = -1e30
+    counts = np.zeros((rows, vocab), dtype=np.uint32)
+    counts[:, 900] = 3
+    counts[:, 100] = 0xFFFFFFFF
+    configs = [W.cfg(0.0, 1.0, 1), W.cfg(0.5, 0.9, 20), W.cfg(0.5, 0.9, 20),
+               W.cfg(0.5, 0.9, 20, presence=0.25), W.cfg(0.5, 1.0, 20),
+               W.cfg(0.5, 1.0, 20), W.cfg(1.0, 0.5, 2, frequency=0.5), W.cfg(0.0, 1.0, 1),
+               W.cfg(0.0, 1.0, 1, repetition=1.2), W.cfg(0.0, 1.0, 1)]
+    logits[8, :] = np.float32(2.0)
+    logits[9, :] = np.float32(-2.0)
+    logits[9, 12] = np.inf
+    w = dict(logits=logits, counts=counts, configs=configs,
+             uniforms=np.linspace(0.05, 0.95, rows).astype(np.float32), logprobs=5)
+    check(w, run_hip(w, dev), W.oracle_run(w), "non-finite")
+
+
+def test_uniform_edges(dev):
+    w = W.config2(rows=6, vocab=5000)
+    w["uniforms"] = np.array([0.0, -1.0, np.nan, 1.0, 2.0, np.float32(0.99999994)],
+                             dtype=np.float32)
+    check(w, run_hip(w, dev), W.oracle_run(w), "uniform edges")
+
+
+def test_strided_rows_and_no_counts(dev):
+    import torch
+    w = W.config2(rows=8, vocab=3001)
+    ref = W.oracle_run(dict(w, counts=np.zeros_like(w["counts"])))
+    s = fg_hip.HipSampler(3001, 8)
+    s.set_configs([fg_hip.make_config(**{"temperature": c["temperature"], "top_p": c["top_p"],
+                                         "top_k": c["top_k"]}) for c in w["configs"]])
+    big = np.zeros((8, 3007), dtype=np.float32)
+    big[:, :3001] = w["logits"]
+    d = to_dev(big, dev)
+    tok = torch.empty(8, dtype=torch.int32, device=dev)
+    st = torch.empty(8, dtype=torch.int32, device=dev)
+    s.sample(d, to_dev(w["uniforms"], dev), tok, row_status=st, logits_stride=3007)
+    torch.cuda.synchronize()
+    assert np.array_equal(st.cpu().numpy(), ref["status"])
+    got = tok.cpu().numpy().view(np.uint32)
+    near = ref["margin"] < BOUNDARY
+    assert np.all((got == ref["token"]) | near)
+
+
+def test_argument_errors(dev):
+    import torch
+    s = fg_hip.HipSampler(100, 4)
+    with pytest.raises(fg_hip.FgStatusError) as e:
+        s.set_configs([fg_hip.make_config(top_k=65)])
+    assert e.value.code == fg_hip.FG_ERR_ARGUMENT
+    with pytest.raises(fg_hip.FgStatusError):
+        s.set_configs([fg_hip.make_config(min_p=0.1)])
+    with pytest.raises(fg_hip.FgStatusError):
+        s.set_configs([fg_hip.make_config(top_k=0)])
+    s.set_configs([fg_hip.make_config()] * 4)
+    x = torch.zeros((4, 100), device=dev)
+    u = torch.zeros(4, device=dev)
+    t = torch.zeros(4, dtype=torch.int32, device=dev)
+    with pytest.raises(fg_hip.FgStatusError):
+        s.sample(x, u, t, rows=5)
+    with pytest.raises(fg_hip.FgStatusError):
+        s.sample(x, u, t, logits_stride=99)
+    with pytest.raises(fg_hip.FgStatusError):
+        s.sample(x, u, t, logprobs=65, logprob_values=x, logprob_ids=t)
+
+
+def test_history_increment(dev):
+    import torch
+    vocab, rows = 1000, 4
+    s = fg_hip.HipSampler(vocab, rows)
+    s.set_configs([fg_hip.make_config(presence=1.0), fg_hip.make_config(),
+                   fg_hip.make_config(repetition=1.1), fg_hip.make_config(frequency=0.1)])
+    counts = torch.zeros((rows, vocab), dtype=torch.int32, device=dev)
+    counts[3, 9] = -1  # UINT32_MAX saturates
+    tokens = torch.tensor([5, 6, 7, 9], dtype=torch.int32, device=dev)
+    status = torch.tensor([0, 0, 4, 0], dtype=torch.int32, device=dev)
+    s.history_increment(counts, tokens, row_status=status)
+    torch.cuda.synchronize()
+    c = counts.cpu().numpy().view(np.uint32)
+    assert c[0, 5] == 1 and c[1, 6] == 0 and c[2, 7] == 0 and c[3, 9] == 0xFFFFFFFF
+    assert c.sum(dtype=np.uint64) == 1 + 0xFFFFFFFF

@@ -1,0 +1,192 @@
+"""GPU parity of the unit entry points that replace the reference's Vulkan
+dispatches: penalties, the argmax ladder and the top-k ladder, plus the
+history table kernels.  Known answers are the reference's own GPU tests
+(tests/test_fg_vk.c:1274-1342)."""
+import numpy as np
+import pytest
+
+import fg_hip
+import oracle_ffi as O
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_f32(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+
+
+def dev_u32(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev)
+
+
+def u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("vocab,offset", [(151_936, 0), (248_320, 0), (1001, 0), (4099, 1)])
+def test_apply_penalties_matches_c_formula(dev, vocab, offset):
+    import torch
+    rng = np.random.default_rng(vocab)
+    x = rng.normal(0, 3, vocab + offset).astype(np.float32)
+    c = np.zeros(vocab + offset, dtype=np.uint32)
+    hot = rng.integers(0, vocab + offset, 5000)
+    c[hot] = rng.integers(1, 1000, hot.size).astype(np.uint32)
+    c[:3] = [0xFFFFFFFF, 7, 1]
+    x[:3] = [-0.0, 0.0, np.nan]
+    dx = dev_f32(x, dev)
+    dc = dev_u32(c, dev)
+    fg_hip.apply_penalties(dx[offset:], dc[offset:], 1.5, 0.3, 1.05)
+    torch.cuda.synchronize()
+    want = O.penalties_c(x[offset:], c[offset:], 1.5, 0.3, 1.05)
+    got = dx[offset:].cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_apply_penalties_rejects_bad_arguments(dev):
+    x = dev_f32(np.zeros(8), dev)
+    c = dev_u32(np.zeros(8), dev)
+    for pres, freq, rep in [(np.nan, 0, 1), (0, np.inf, 1), (0, 0, 0.0), (0, 0, -1.0)]:
+        with pytest.raises(fg_hip.FgStatusError) as e:
+            fg_hip.apply_penalties(x, c, pres, freq, rep)
+        assert e.value.code == fg_hip.FG_ERR_ARGUMENT
+
+
+def ladder_argmax(scores, dev):
+    import torch
+    n = scores.size
+    cur_s = dev_f32(scores, dev)
+    cur_i = None
+    while n > 1:
+        g = (n + 4095) // 4096
+        os_ = torch.empty(g, dtype=torch.float32, device=dev)
+        oi = torch.empty(g, dtype=torch.int32, device=dev)
+        n = fg_hip.argmax_reduce(os_, oi, cur_s, cur_i, n)
+        cur_s, cur_i = os_, oi
+    torch.cuda.synchronize()
+    return float(cur_s.cpu()[0]), int(u32(cur_i)[0]) if cur_i is not None else 0
+
+
+def test_argmax_known_answers(dev):
+    """tests/test_fg_vk.c:1340-1342: s_i = -i, s[12345] = s[23456] = 100 -> 12345;
+    then s[45678] = NaN -> 45678 (non-finite ranks first)."""
+    n = 248_320
+    s = -np.arange(n, dtype=np.float32)
+    s[12345] = 100.0
+    s[23456] = 100.0
+    v, i = ladder_argmax(s, dev)
+    assert (i, v) == (12345, 100.0)
+    s[45678] = np.nan
+    v, i = ladder_argmax(s, dev)
+    assert i == 45678 and not np.isfinite(v)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_argmax_step_matches_oracle(dev, seed):
+    import torch
+    rng = np.random.default_rng(seed)
+    n = 50_000 + seed * 777
+    s = np.round(rng.normal(0, 2, n), 1).astype(np.float32)  # many ties
+    ids = rng.permutation(n).astype(np.uint32)
+    ids[::97] = 0xFFFFFFFF  # padding entries
+    if seed == 1:
+        s[rng.integers(0, n, 20)] = np.inf
+    if seed == 2:
+        s[:] = 0.0
+        s[::2] = -0.0
+    g = (n + 4095) // 4096
+    os_ = torch.empty(g, dtype=torch.float32, device=dev)
+    oi = torch.empty(g, dtype=torch.int32, device=dev)
+    assert fg_hip.argmax_reduce(os_, oi, dev_f32(s, dev), dev_u32(ids, dev), n) == g
+    torch.cuda.synchronize()
+    ws, wi = O.argmax_reduce_step(s, ids)
+    assert np.array_equal(u32(oi), wi)
+    assert np.array_equal(os_.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+
+
+def test_topk_known_answers(dev):
+    """tests/test_fg_vk.c:1274-1338."""
+    import torch
+    scores = np.array([1, 9, 7, 9, 3, 8, 2, 7, 6, 5, 4, 0, -1, -2, -3, -4, -5, -6, np.nan],
+                      dtype=np.float32)
+    ids = np.arange(19, dtype=np.uint32)
+    ds, di = dev_f32(scores, dev), dev_u32(ids, dev)
+    os_ = torch.empty(4, dtype=torch.float32, device=dev)
+    oi = torch.empty(4, dtype=torch.int32, device=dev)
+    for bad_k in (0, 65):
+        with pytest.raises(fg_hip.FgStatusError) as e:
+            fg_hip.topk_select(os_, oi, ds, di, 19, bad_k)
+        assert e.value.code == fg_hip.FG_ERR_ARGUMENT
+    assert fg_hip.topk_select(os_, oi, ds, di, 19, 4) == 4
+    torch.cuda.synchronize()
+    got_i, got_s = u32(oi), os_.cpu().numpy()
+    assert sorted(got_i.tolist()) == [1, 2, 3, 5]
+    assert np.array_equal(got_s, scores[got_i])
+    first = (got_i.copy(), got_s.copy())
+    fg_hip.topk_select(os_, oi, ds, di, 19, 4)
+    torch.cuda.synchronize()
+    assert np.array_equal(u32(oi), first[0]) and np.array_equal(os_.cpu().numpy(), first[1])
+    assert fg_hip.topk_select(os_, oi, ds, di, 19, 1) == 1
+    torch.cuda.synchronize()
+    assert u32(oi)[0] == 1 and os_.cpu().numpy()[0] == 9.0  # tie 9.0 at ids 1, 3
+    short = np.full(19, np.nan, dtype=np.float32)
+    short[1], short[3] = 9.0, 8.0
+    assert fg_hip.topk_select(os_, oi, dev_f32(short, dev), di, 19, 4) == 4
+    torch.cuda.synchronize()
+    gi, gs = u32(oi), os_.cpu().numpy()
+    assert gi[0] != 0xFFFFFFFF and gi[1] != 0xFFFFFFFF and gi[2] == 0xFFFFFFFF
+    assert not np.isfinite(gs[2])
+
+
+@pytest.mark.parametrize("k", [1, 4, 20, 50, 64])
+def test_topk_step_and_ladder_match_oracle(dev, k):
+    import torch
+    rng = np.random.default_rng(k)
+    n = 151_936
+    s = np.round(rng.normal(0, 3, n) * 4) / 4
+    s = s.astype(np.float32)
+    s[rng.integers(0, n, 100)] = np.nan
+    s[rng.integers(0, n, 100)] = -np.inf
+    s[5000:5100] = 0.0
+    s[5100:5200] = -0.0
+    tiles = (n + 1023) // 1024
+    os_ = torch.empty(tiles * k, dtype=torch.float32, device=dev)
+    oi = torch.empty(tiles * k, dtype=torch.int32, device=dev)
+    ds = dev_f32(s, dev)
+    produced = fg_hip.topk_select(os_, oi, ds, None, n, k)
+    torch.cuda.synchronize()
+    ws, wi = O.topk_select_step(s, k)
+    assert produced == ws.size
+    assert np.array_equal(u32(oi), wi)
+    assert np.array_equal(os_.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+    # Ladder to a fixed point (src/output.c:681-700) = exact top-k by key.
+    cur_s, cur_i, count = os_, oi, produced
+    while count > k:
+        t = (count + 1023) // 1024
+        ns = torch.empty(t * k, dtype=torch.float32, device=dev)
+        ni = torch.empty(t * k, dtype=torch.int32, device=dev)
+        count = fg_hip.topk_select(ns, ni, cur_s, cur_i, count, k)
+        cur_s, cur_i = ns, ni
+    torch.cuda.synchronize()
+    rs, ri, have = O.topk_row(s, k)
+    assert sorted(u32(cur_i).tolist()) == sorted(ri.tolist())
+
+
+def test_history_build_matches_oracle(dev):
+    import torch
+    rows, vocab = 6, 151_936
+    ids = O.gen_zipf_ids(rows, 1024, vocab, 1.1, 7, 7)
+    want = O.build_counts(ids, vocab)
+    d = torch.full((rows, vocab + 8), 123, dtype=torch.int32, device=dev)
+    offsets = torch.arange(0, (rows + 1) * 1024, 1024, dtype=torch.int64, device=dev)
+    fg_hip.history_build(d, vocab + 8, vocab, dev_u32(ids.reshape(-1), dev), offsets, rows)
+    got = u32(d)
+    assert np.array_equal(got[:, :vocab], want)
+    assert (got[:, vocab:] == 123).all()
+    bad = ids.reshape(-1).copy()
+    bad[100] = vocab
+    with pytest.raises(fg_hip.FgStatusError) as e:
+        fg_hip.history_build(d, vocab + 8, vocab, dev_u32(bad, dev), offsets, rows)
+    assert e.value.code == fg_hip.FG_ERR_FORMAT
