@@ -87,76 +87,197 @@ __device__ __forceinline__ float penalise(float s, uint32_t c, float pres, float
   return s - total;
 }
 
-// ---- wave reductions --------------------------------------------------------
+// ---- cross-lane exchanges in VALU (DPP and gfx950 permlane swaps) ----------
+//
+// lane_xor<J>(v) returns v of lane (lane ^ J).  J = 1, 2: quad_perm; 4: the
+// half-row mirror (^7) followed by the quad mirror (^3); 8: row rotate by 8;
+// 16, 32: v_permlane16/32_swap, which hand every lane both members of its pair.
+
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xf, 0xf, false));
+}
+
+template <int J>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  if constexpr (J == 1) {
+    return dpp<0xB1>(v);
+  } else if constexpr (J == 2) {
+    return dpp<0x4E>(v);
+  } else if constexpr (J == 4) {
+    return dpp<0x1B>(dpp<0x141>(v));
+  } else if constexpr (J == 8) {
+    return dpp<0x128>(v);
+  } else if constexpr (J == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane_id() & 16u) ? r[0] : r[1];
+  } else {
+    static_assert(J == 32, "lane_xor: J must be a power of two below 64");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane_id() & 32u) ? r[0] : r[1];
+  }
+}
+
+template <int J>
+__device__ __forceinline__ uint64_t lane_xor64(uint64_t v) {
+  const uint32_t lo = lane_xor<J>(static_cast<uint32_t>(v));
+  const uint32_t hi = lane_xor<J>(static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// v of lane 63 - lane.
+__device__ __forceinline__ uint32_t lane_reverse(uint32_t v) {
+  return lane_xor<32>(lane_xor<16>(dpp<0x140>(v)));
+}
+__device__ __forceinline__ uint64_t lane_reverse64(uint64_t v) {
+  const uint32_t lo = lane_reverse(static_cast<uint32_t>(v));
+  const uint32_t hi = lane_reverse(static_cast<uint32_t>(v >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, uint32_t lane) {
+  const uint32_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), static_cast<int>(lane)));
+  const uint32_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), static_cast<int>(lane)));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ uint32_t readlane32(uint32_t v, uint32_t lane) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(lane)));
+}
+
+// One compare-exchange step of a bitonic network over the 64 lanes: blocks of
+// K lanes, partner at distance J; the final order is descending by lane.
+template <int K, int J, typename T>
+__device__ __forceinline__ T bitonic_step(T v) {
+  T o;
+  if constexpr (sizeof(T) == 8) o = lane_xor64<J>(v);
+  else o = lane_xor<J>(v);
+  const uint32_t lane = lane_id();
+  const bool desc = (K == kWave) || ((lane & K) == 0);
+  const bool lower = (lane & J) == 0;
+  const T hi = o > v ? o : v;
+  const T lo = o > v ? v : o;
+  return (lower == desc) ? hi : lo;
+}
+
+template <int K, typename T>
+__device__ __forceinline__ T bitonic_merge_stage(T v) {
+  if constexpr (K >= 64) v = bitonic_step<K, 32>(v);
+  if constexpr (K >= 32) v = bitonic_step<K, 16>(v);
+  if constexpr (K >= 16) v = bitonic_step<K, 8>(v);
+  if constexpr (K >= 8) v = bitonic_step<K, 4>(v);
+  if constexpr (K >= 4) v = bitonic_step<K, 2>(v);
+  return bitonic_step<K, 1>(v);
+}
+
+// Sorts one value per lane across the wave, descending (lane 0 the largest).
+template <typename T>
+__device__ __forceinline__ T wave_sort_desc(T v) {
+  v = bitonic_merge_stage<2>(v);
+  v = bitonic_merge_stage<4>(v);
+  v = bitonic_merge_stage<8>(v);
+  v = bitonic_merge_stage<16>(v);
+  v = bitonic_merge_stage<32>(v);
+  return bitonic_merge_stage<64>(v);
+}
+__device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t v) { return wave_sort_desc(v); }
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) { return wave_sort_desc(v); }
+
+// a and b are descending across the lanes; returns the 64 largest of both,
+// descending.  max(a_i, b_{63-i}) is bitonic and holds the 64 largest.
+__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t a, uint64_t b) {
+  const uint64_t r = lane_reverse64(b);
+  return bitonic_merge_stage<64>(a > r ? a : r);
+}
+
+// ---- wave reductions and scans ------------------------------------------------
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint64_t o = __shfl_xor(v, d);
-    v = o > v ? o : v;
-  }
-  return v;
+  v = max(v, lane_xor64<1>(v));
+  v = max(v, lane_xor64<2>(v));
+  v = max(v, lane_xor64<4>(v));
+  v = max(v, lane_xor64<8>(v));
+  v = max(v, lane_xor64<16>(v));
+  return max(v, lane_xor64<32>(v));
 }
 
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint64_t o = __shfl_xor(v, d);
-    v = o < v ? o : v;
-  }
-  return v;
+  v = min(v, lane_xor64<1>(v));
+  v = min(v, lane_xor64<2>(v));
+  v = min(v, lane_xor64<4>(v));
+  v = min(v, lane_xor64<8>(v));
+  v = min(v, lane_xor64<16>(v));
+  return min(v, lane_xor64<32>(v));
 }
 
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
-  return v;
+template <int J>
+__device__ __forceinline__ double lane_xor_f64(double x) {
+  return __longlong_as_double(static_cast<long long>(
+      lane_xor64<J>(static_cast<uint64_t>(__double_as_longlong(x)))));
 }
 
-// Inclusive sum over lanes >= this lane.
+__device__ __forceinline__ double wave_max_f64(double x) {
+  x = fmax(x, lane_xor_f64<1>(x));
+  x = fmax(x, lane_xor_f64<2>(x));
+  x = fmax(x, lane_xor_f64<4>(x));
+  x = fmax(x, lane_xor_f64<8>(x));
+  x = fmax(x, lane_xor_f64<16>(x));
+  return fmax(x, lane_xor_f64<32>(x));
+}
+
+// Butterfly sum: every lane ends with the same total.
+__device__ __forceinline__ double wave_sum_f64(double x) {
+  x += lane_xor_f64<1>(x);
+  x += lane_xor_f64<2>(x);
+  x += lane_xor_f64<4>(x);
+  x += lane_xor_f64<8>(x);
+  x += lane_xor_f64<16>(x);
+  return x + lane_xor_f64<32>(x);
+}
+
+// v of lane (lane - D) inside each row of 16 lanes, 0 for the first D lanes
+// of a row (DPP row_shr with bound_ctrl).
+template <int D>
+__device__ __forceinline__ uint32_t row_shr(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x110 + D, 0xf, 0xf, true));
+}
+
+template <int D>
+__device__ __forceinline__ double row_shr_f64(double x) {
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(x));
+  const uint32_t lo = row_shr<D>(static_cast<uint32_t>(b));
+  const uint32_t hi = row_shr<D>(static_cast<uint32_t>(b >> 32));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// Inclusive prefix sum over lanes 0..lane: a row-local Hillis-Steele scan,
+// then each row adds the totals of the rows before it (read with readlane).
+__device__ __forceinline__ double wave_prefix_sum_f64(double x) {
+  x += row_shr_f64<1>(x);
+  x += row_shr_f64<2>(x);
+  x += row_shr_f64<4>(x);
+  x += row_shr_f64<8>(x);
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(x));
+  const double r0 = __longlong_as_double(static_cast<long long>(readlane64(b, 15)));
+  const double r1 = __longlong_as_double(static_cast<long long>(readlane64(b, 31)));
+  const double r2 = __longlong_as_double(static_cast<long long>(readlane64(b, 47)));
+  const uint32_t row = lane_id() >> 4;
+  const double before = row == 0 ? 0.0 : row == 1 ? r0 : row == 2 ? r0 + r1 : (r0 + r1) + r2;
+  return x + before;
+}
+
+// Inclusive sum over lanes >= this lane (used by the LDS radix select).
 __device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t v) {
   const uint32_t lane = lane_id();
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
     const uint32_t o = __shfl_down(v, d);
     if (lane + d < kWave) v += o;
-  }
-  return v;
-}
-
-// Bitonic sort of one u64 per lane across the wave, descending (lane 0 holds
-// the largest).
-__device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t v) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int k = 2; k <= kWave; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j >= 1; j >>= 1) {
-      const uint64_t o = __shfl_xor(v, j);
-      // Within each k-block the final stage runs descending; blocks alternate.
-      const bool desc = ((lane & k) == 0);
-      const bool lower = ((lane & j) == 0);
-      const bool take_max = (lower == desc);
-      const uint64_t hi = o > v ? o : v;
-      const uint64_t lo = o > v ? v : o;
-      v = take_max ? hi : lo;
-    }
-  }
-  return v;
-}
-
-__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int k = 2; k <= kWave; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j >= 1; j >>= 1) {
-      const uint32_t o = __shfl_xor(v, j);
-      const bool desc = ((lane & k) == 0);
-      const bool lower = ((lane & j) == 0);
-      const bool take_max = (lower == desc);
-      v = take_max ? (o > v ? o : v) : (o > v ? v : o);
-    }
   }
   return v;
 }

@@ -1,23 +1,28 @@
-// gfx950 kernels of the batched sampler: one fused streaming pass over
+// gfx950 kernel of the batched sampler: one fused streaming pass over
 // rows x vocab f32 logits (+ u32 history counts) that ends in a token per row.
 //
 // Grid: rows x chunks workgroups of 256 threads (4 waves).  Each wave streams
-// a contiguous slice of its row once from HBM (16-byte non-temporal loads of
-// logits and counts) and keeps in registers/LDS only what the row result
-// needs:
+// a contiguous slice of its row from HBM exactly once: 16-byte non-temporal
+// loads of logits and counts, double-buffered so the next step's loads are in
+// flight while the current step is processed.  In registers each wave keeps
+// only what the row's result needs:
 //   * penalties (src/sampler.c:55-58) applied in registers;
 //   * greedy: the best greedy composite (src/output.c:484-492);
-//   * top-k:  an LDS candidate buffer filtered by a rising composite
-//             threshold, cut back to the exact top-kk by an LDS radix select
-//             when it fills (the per-tile radix idea of
-//             shaders/fg_topk_select.comp:45-77, applied per wave);
+//   * top-k:  a sorted register list of its best 64 composites behind a
+//             rising filter; candidates that pass are staged in LDS and merged
+//             64 at a time with bitonic networks built from DPP / permlane
+//             moves (the reference's per-tile select, shaders/fg_topk_select.comp,
+//             recast as a streaming merge);
 //   * log-probs: per-lane online (max, sum exp) in f32.
-// Each workgroup merges its 4 waves, publishes a sorted top-kk list, its
-// greedy winner and its (max, sum) to the workspace, raises the row's key
-// threshold (a lower bound on the row's kk-th key) and bumps the row's
-// arrival counter.  The last workgroup of a row merges the row and runs the
-// select arithmetic of src/sampler.c:80-122 in one wave, then resets the row's
-// counter and threshold for the next launch.
+// Row hand-off: when a row spans several workgroups, every wave publishes its
+// top-kk list, greedy winner and (max, sum) with device-coherent (sc1) stores
+// and waits for them; the workgroup then bumps the row's arrival counter (one
+// cache line per row, so rows never contend).  The last workgroup to arrive
+// reads the row's partials with sc1 loads, merges the sorted lists and runs
+// the select arithmetic of src/sampler.c:80-122 in one wave, then resets the
+// row's counter for the next launch.  No L2 write-back or invalidate is
+// needed.  A row that fits one workgroup is
+// merged straight from LDS.
 #pragma once
 
 #include "fg_device.hpp"
@@ -38,10 +43,14 @@ constexpr uint32_t kRowPenalties = 1u;
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr uint32_t kCap = 256;       // per-wave candidate buffer (composites)
+constexpr int kStepVec = 4;  // quads (4 elements) per lane per streaming step
+constexpr uint32_t kStepQuads = kWave * kStepVec;
+constexpr uint32_t kStepElems = kStepQuads * 4u;
+// LDS staging per wave: fewer than 64 left over plus one full step.
+constexpr uint32_t kCap = 64u + kStepElems;
 constexpr uint32_t kMaxK = 64;       // largest top-k / log-prob count
-constexpr uint32_t kMaxChunks = 64;  // workgroups per row (one lane each in merges)
-constexpr int kStepVec = 4;          // float4 per lane per streaming step
+constexpr uint32_t kMaxChunks = 64;  // workgroups per row
+constexpr uint32_t kLineWords = 32;  // u32 per 128-byte cache line (row counters)
 
 constexpr int32_t kStOk = 0;
 constexpr int32_t kStFormat = 4;
@@ -65,93 +74,84 @@ struct SampleArgs {
   float* penalised;
   float* lp_values;
   uint32_t* lp_ids;
-  // workspace
-  uint64_t* cand;        // [rows][chunks][kMaxK] sorted composites, 0 = empty
-  uint64_t* greedy;      // [rows][chunks] greedy composites
-  double* lse;           // [rows][chunks][2] (max s, sum exp((s - max)/T))
-  uint32_t* row_thr;     // [rows] key lower bound, reset by the last workgroup
-  uint32_t* row_done;    // [rows] arrivals, reset by the last workgroup
+  // workspace, indexed by wave slot = (row * chunks + chunk) * kWaves + wave
+  uint64_t* cand;        // [slot][kMaxK] top-kk composites of the wave, descending, 0 = empty
+  uint64_t* greedy;      // [slot] greedy composite
+  double* lse;           // [slot][2] (max s, sum exp((s - max)/T))
+  uint32_t* row_done;    // [rows * kLineWords] arrivals, one cache line per row,
+                         // reset by the last workgroup
 };
 
-// ---- per-wave candidate buffer --------------------------------------------
-
-struct Cand {
-  uint64_t* buf;   // kCap composites, wave-private LDS
-  uint32_t* hist;  // 256 u32, wave-private LDS
-  uint32_t n;      // entries in buf (wave-uniform)
-  uint64_t R;      // pass iff composite > R (wave-uniform)
-  uint32_t kk;     // how many to keep
-};
-
-// Cuts the buffer back to its exact top-kk and raises the threshold to the
-// kk-th composite: anything not above it can never enter the top-kk.
-__device__ inline void cand_reduce(Cand& c) {
-  if (c.n <= c.kk) return;
-  const uint64_t R = wave_select_kth(c.buf, c.n, c.kk, c.hist);
-  c.n = wave_compact_ge(c.buf, c.n, R);
-  if (R > c.R) c.R = R;
+// Device-coherent (sc1) accesses for the cross-workgroup hand-off.
+template <typename T>
+__device__ __forceinline__ void store_coherent(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T load_coherent(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent_f64(double* p, double v) {
+  store_coherent(reinterpret_cast<uint64_t*>(p), static_cast<uint64_t>(__double_as_longlong(v)));
+}
+__device__ __forceinline__ double load_coherent_f64(const double* p) {
+  return __longlong_as_double(
+      static_cast<long long>(load_coherent(reinterpret_cast<const uint64_t*>(p))));
+}
+// Waits until this wave's memory operations have completed; the signal
+// fences keep the compiler from moving memory operations across the wait.
+__device__ __forceinline__ void wait_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__device__ __forceinline__ void cand_push(Cand& c, uint64_t comp) {
-  bool pass = comp > c.R;
-  uint64_t m = ballot(pass);
+// ---- per-wave top list ------------------------------------------------------
+//
+// Each wave keeps its best 64 composites so far as one sorted register list
+// (lane i holds the i-th best, descending; 0 = empty).  Streamed candidates
+// that beat the filter R are staged in wave-private LDS; every 64 staged
+// entries are sorted across the lanes and merged into the list.  R rises to
+// the list's kk-th entry after each merge: nothing at or below it can enter
+// the top-kk.
+
+struct TopList {
+  uint64_t top;    // lane i: i-th best composite
+  uint64_t R;      // filter: a candidate must be > R (wave-uniform)
+  uint64_t* buf;   // kCap staged composites (wave-private LDS)
+  uint32_t n;      // staged entries (wave-uniform)
+  uint32_t kk;     // entries of the list that matter (1..64)
+};
+
+__device__ __forceinline__ void top_merge_sorted(TopList& t, uint64_t sorted_desc) {
+  t.top = wave_merge_desc(t.top, sorted_desc);
+  const uint64_t kth = readlane64(t.top, t.kk - 1u);
+  if (kth > t.R) t.R = kth;
+}
+
+// Moves staged entries into the list: whole groups of 64, or everything when
+// `all` is set.
+__device__ __forceinline__ void top_drain(TopList& t, bool all) {
+  const uint32_t lane = lane_id();
+  while (t.n >= static_cast<uint32_t>(kWave) || (all && t.n > 0u)) {
+    const uint32_t take = t.n < static_cast<uint32_t>(kWave) ? t.n : static_cast<uint32_t>(kWave);
+    const uint32_t at = t.n - take;
+    uint64_t x = lane < take ? t.buf[at + lane] : 0ull;
+    wave_lds_sync();
+    t.n = at;
+    if (x <= t.R) x = 0ull;  // beaten by a list that grew after it was staged
+    if (ballot(x != 0ull) == 0ull) continue;
+    top_merge_sorted(t, wave_sort_desc(x));
+  }
+}
+
+// Stages this lane's composite if it beats R.  The caller keeps n + 64 <= kCap.
+__device__ __forceinline__ void top_stage(TopList& t, uint64_t comp) {
+  const bool pass = comp > t.R;
+  const uint64_t m = ballot(pass);
   if (m == 0ull) return;
-  if (c.n + static_cast<uint32_t>(__popcll(m)) > kCap) {
-    cand_reduce(c);
-    pass = comp > c.R;
-    m = ballot(pass);
-    if (m == 0ull) return;
-  }
-  if (pass) c.buf[c.n + lanes_below(m)] = comp;
-  c.n += static_cast<uint32_t>(__popcll(m));
-}
-
-// Wave 0 of a workgroup: gathers the 4 wave buffers (each <= kk entries) into
-// buffer 0, cuts to the exact top-kk and returns this lane's entry of the
-// descending list (0 past the end).  *count receives the list length.
-__device__ inline uint64_t wave0_merge(uint64_t (*bufs)[kCap], const uint32_t* ns, uint32_t* hist,
-                                       uint32_t kk, uint32_t* count) {
-  const uint32_t lane = lane_id();
-  uint32_t n = ns[0];
-  for (int w = 1; w < kWaves; w++) {
-    const uint32_t m = ns[w];
-    for (uint32_t i = lane; i < m; i += kWave) bufs[0][n + i] = bufs[w][i];
-    n += m;
-  }
-  wave_lds_sync();
-  if (n > kk) {
-    const uint64_t R = wave_select_kth(bufs[0], n, kk, hist);
-    n = wave_compact_ge(bufs[0], n, R);
-  }
-  wave_lds_sync();
-  const uint64_t mine = lane < n ? bufs[0][lane] : 0ull;
-  *count = n;
-  return wave_sort_desc_u64(mine);
-}
-
-__device__ __forceinline__ double wave_prefix_sum_f64(double x) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const double o = __shfl_up(x, d);
-    if (lane >= static_cast<uint32_t>(d)) x += o;
-  }
-  return x;
-}
-
-__device__ __forceinline__ double wave_max_f64(double x) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const double o = __shfl_xor(x, d);
-    x = o > x ? o : x;
-  }
-  return x;
-}
-
-__device__ __forceinline__ double wave_sum_f64(double x) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d);
-  return x;
+  if (pass) t.buf[t.n + lanes_below(m)] = comp;
+  t.n += static_cast<uint32_t>(__popcll(m));
 }
 
 // Value order of src/sampler.c:75-78 (value desc, id asc) as a composite:
@@ -163,13 +163,234 @@ __device__ __forceinline__ uint64_t value_comp_from(uint64_t key_comp) {
   return (static_cast<uint64_t>(k) << 32) | (key_comp & 0xffffffffull);
 }
 
+// A key-ordered list re-ordered by value: only -0 entries can move.
+__device__ __forceinline__ uint64_t value_order(uint64_t key_sorted) {
+  const uint64_t v = value_comp_from(key_sorted);
+  if (ballot(key_sorted != 0ull && comp_key(key_sorted) == 0x7fffffffu) == 0ull) return v;
+  return wave_sort_desc(v);
+}
+
+// Combines per-lane (max s, sum exp((s - max)/T)) pairs of a wave in f64.
+__device__ __forceinline__ void wave_lse_combine(double m, double z, double t, double* wm,
+                                                 double* wz) {
+  const double mm = wave_max_f64(m);
+  const double zz = (m == -INFINITY) ? 0.0 : z * exp((m - mm) / t);
+  *wm = mm;
+  *wz = wave_sum_f64(zz);
+}
+
+// ---- the row's final step (one wave) ---------------------------------------
+
+// fin: lane i holds the row's i-th best composite in key order (0 past the
+// end); gbest: the row's greedy composite; (m, z): the row's log-sum-exp
+// partial.  Writes token, logit, status and log-probs of the row.
+__device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint32_t row,
+                                  uint64_t fin, uint64_t gbest, double m, double z,
+                                  const float* lrow, const uint32_t* crow, bool pen) {
+  const uint32_t lane = lane_id();
+  const bool greedy = p.temperature == 0.0f;
+  const uint32_t L = a.logprobs;
+  const uint32_t kk = greedy ? L : (p.top_k > L ? p.top_k : L);
+  fin = lane < kk ? fin : 0ull;  // past kk the lists are not exact
+  int32_t status = kStOk;
+  uint32_t token = kInvalidId;
+  float token_logit = -INFINITY;
+
+  if (greedy) {
+    // src/output.c:560-599 / 728-741: a non-finite winner is an error.
+    const uint32_t id = comp_id(gbest);
+    float v = -INFINITY;
+    if (gbest != 0ull && id < a.vocab) {
+      v = lrow[id];
+      if (pen) v = penalise(v, crow[id], p.presence, p.frequency, p.repetition);
+    }
+    token_logit = v;
+    if (gbest == 0ull || !is_finite_bits(__float_as_uint(v)))
+      status = pen ? kStFormat : kStMismatch;
+    else
+      token = id;
+  } else {
+    // fg_sampler_select (src/sampler.c:80-122) over the exact top_k, in value
+    // order; the f64 running sums are parallel prefix sums.
+    const uint32_t topk = p.top_k;
+    const uint64_t sorted = value_order(lane < topk ? fin : 0ull);
+    const uint32_t kept = static_cast<uint32_t>(__popcll(ballot(sorted != 0ull)));
+    if (kept == 0u) {
+      status = kStFormat;
+    } else {
+      const uint32_t limit = topk < kept ? topk : kept;
+      const bool live = lane < limit;
+      const double v = live ? static_cast<double>(key_to_float(comp_key(sorted))) : 0.0;
+      const double vmax = __longlong_as_double(static_cast<long long>(
+          readlane64(static_cast<uint64_t>(__double_as_longlong(v)), 0)));
+      const double e = live ? exp(v - vmax) : 0.0;
+      const double ecum = wave_prefix_sum_f64(e);
+      const double sum = __longlong_as_double(static_cast<long long>(
+          readlane64(static_cast<uint64_t>(__double_as_longlong(ecum)), limit - 1u)));
+      if (!(sum > 0.0) || !isfinite(sum)) {
+        status = kStFormat;
+      } else {
+        const double cum = wave_prefix_sum_f64(e / sum);
+        const uint64_t hit = ballot(live && cum >= static_cast<double>(p.top_p));
+        const uint32_t cutoff = hit ? static_cast<uint32_t>(__builtin_ctzll(hit)) + 1u : limit;
+        const double t = static_cast<double>(p.temperature);
+        const double vmax_t = vmax / t;
+        const double te = lane < cutoff ? exp(v / t - vmax_t) : 0.0;
+        const double tcum = wave_prefix_sum_f64(te);
+        const double tsum = __longlong_as_double(static_cast<long long>(
+            readlane64(static_cast<uint64_t>(__double_as_longlong(tcum)), cutoff - 1u)));
+        if (!(tsum > 0.0) || !isfinite(tsum)) {
+          status = kStFormat;
+        } else {
+          float u = a.uniforms[row];
+          if (!is_finite_bits(__float_as_uint(u)) || u < 0.0f) u = 0.0f;
+          if (u >= 1.0f) u = __uint_as_float(0x3f7fffffu);  // nextafterf(1, 0)
+          const double draw = static_cast<double>(u) * tsum;
+          const uint64_t hit2 = ballot(lane < cutoff && draw < tcum);
+          const uint32_t pick = hit2 ? static_cast<uint32_t>(__builtin_ctzll(hit2)) : cutoff - 1u;
+          token = comp_id(readlane64(sorted, pick));
+          // The logit keeps its sign of zero: read it from the key-order list.
+          const uint64_t owner = ballot(fin != 0ull && comp_id(fin) == token);
+          token_logit = key_to_float(
+              comp_key(readlane64(fin, static_cast<uint32_t>(__builtin_ctzll(owner)))));
+        }
+      }
+    }
+  }
+
+  if (L) {
+    const double te = static_cast<double>(p.temperature > 0.0f ? p.temperature : 1.0f);
+    const double lse = m / te + log(z);
+    const uint64_t vs = value_order(fin);
+    if (lane < L) {
+      float lp = -INFINITY;
+      uint32_t id = kInvalidId;
+      if (vs != 0ull) {
+        id = comp_id(vs);
+        lp = static_cast<float>(static_cast<double>(key_to_float(comp_key(vs))) / te - lse);
+      }
+      a.lp_values[static_cast<uint64_t>(row) * L + lane] = lp;
+      a.lp_ids[static_cast<uint64_t>(row) * L + lane] = id;
+    }
+  }
+  if (lane == 0) {
+    a.tokens[row] = token;
+    if (a.token_logits) a.token_logits[row] = token_logit;
+    if (a.row_status) a.row_status[row] = status;
+  }
+}
+
+// ---- streaming ---------------------------------------------------------------
+
+template <bool kVec>
+__device__ __forceinline__ void load_quad(const float* lrow, const uint32_t* crow, bool pen,
+                                          uint32_t q, f4& x, u4& y) {
+  const uint32_t i = q * 4u;
+  if (kVec) {
+    x = __builtin_nontemporal_load(reinterpret_cast<const f4*>(lrow + i));
+    y = pen ? __builtin_nontemporal_load(reinterpret_cast<const u4*>(crow + i))
+            : u4{0u, 0u, 0u, 0u};
+  } else {
+    x = f4{lrow[i], lrow[i + 1], lrow[i + 2], lrow[i + 3]};
+    y = pen ? u4{crow[i], crow[i + 1], crow[i + 2], crow[i + 3]} : u4{0u, 0u, 0u, 0u};
+  }
+}
+
+struct WaveState {
+  TopList t;
+  uint64_t gbest;
+  float lm;  // per-lane max of finite s
+  float lz;  // per-lane sum exp2((s - lm) * log2e / T)
+  bool first;
+};
+
+// One streaming step: x/y hold quads q0 + j*64 + lane (j < kStepVec); quads
+// at or past q_end are clamped duplicates and are masked out.
+__device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, bool pen,
+                                             bool greedy, uint32_t L, float log2e_over_t,
+                                             float* prow, const f4* x, const u4* y, uint32_t q0,
+                                             uint32_t q_end) {
+  const uint32_t lane = lane_id();
+  float v[kStepVec][4];
+  bool ok[kStepVec];
+#pragma unroll
+  for (int j = 0; j < kStepVec; j++) {
+    const uint32_t q = q0 + j * kWave + lane;
+    ok[j] = q < q_end;
+    v[j][0] = x[j].x;
+    v[j][1] = x[j].y;
+    v[j][2] = x[j].z;
+    v[j][3] = x[j].w;
+    if (pen) {
+      v[j][0] = penalise(v[j][0], y[j].x, p.presence, p.frequency, p.repetition);
+      v[j][1] = penalise(v[j][1], y[j].y, p.presence, p.frequency, p.repetition);
+      v[j][2] = penalise(v[j][2], y[j].z, p.presence, p.frequency, p.repetition);
+      v[j][3] = penalise(v[j][3], y[j].w, p.presence, p.frequency, p.repetition);
+    }
+    if (prow && ok[j]) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) prow[q * 4u + e] = v[j][e];
+    }
+  }
+  uint32_t lane_max_key = 0u;
+  float step_max = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kStepVec; j++) {
+    const uint32_t q = q0 + j * kWave + lane;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
+      if (greedy) {
+        const uint64_t g = greedy_comp(v[j][e], ok[j] ? q * 4u + e : kInvalidId);
+        st.gbest = g > st.gbest ? g : st.gbest;
+      }
+      if (key) {
+        lane_max_key = key > lane_max_key ? key : lane_max_key;
+        step_max = fmaxf(step_max, v[j][e]);
+      }
+    }
+  }
+  if (L) {
+    if (step_max > st.lm) {
+      st.lz = (st.lm == -INFINITY) ? 0.0f : st.lz * exp2f((st.lm - step_max) * log2e_over_t);
+      st.lm = step_max;
+    }
+#pragma unroll
+    for (int j = 0; j < kStepVec; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (ok[j] && is_finite_bits(__float_as_uint(v[j][e])))
+          st.lz += exp2f((v[j][e] - st.lm) * log2e_over_t);
+  }
+  if (st.t.kk) {
+    if (st.first) {
+      // The kk-th largest lane maximum: at least kk keys of this step are >=
+      // it, so it bounds the wave's kk-th key from below.
+      const uint32_t sorted = wave_sort_desc_u32(lane_max_key);
+      const uint32_t T = readlane32(sorted, st.t.kk - 1u);
+      const uint64_t R = T ? ((static_cast<uint64_t>(T) << 32) - 1ull) : 0xffffffffull;
+      if (R > st.t.R) st.t.R = R;
+      st.first = false;
+    }
+#pragma unroll
+    for (int j = 0; j < kStepVec; j++) {
+      const uint32_t q = q0 + j * kWave + lane;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
+        top_stage(st.t, make_comp(key, q * 4u + e));
+      }
+    }
+    top_drain(st.t, false);
+  }
+}
+
 // ---- the fused kernel ------------------------------------------------------
 
 template <bool kVec>
 __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   __shared__ uint64_t s_buf[kWaves][kCap];
-  __shared__ uint32_t s_hist[kWaves][256];
-  __shared__ uint32_t s_n[kWaves];
+  __shared__ uint64_t s_top[kWaves][kWave];
   __shared__ uint64_t s_greedy[kWaves];
   __shared__ double s_lm[kWaves];
   __shared__ double s_lz[kWaves];
@@ -191,284 +412,173 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint32_t* crow = pen ? a.counts + static_cast<uint64_t>(row) * a.cstride : nullptr;
   float* prow = a.penalised ? a.penalised + static_cast<uint64_t>(row) * a.vocab : nullptr;
 
-  const uint32_t wbegin = (chunk * kWaves + wave) * a.wave_elems;
+  const uint32_t wbegin = min((chunk * kWaves + wave) * a.wave_elems, a.vocab);
   const uint32_t wend = min(wbegin + a.wave_elems, a.vocab);
+  const uint32_t q_begin = wbegin / 4u;
+  const uint32_t q_end = (wbegin + ((wend - wbegin) & ~3u)) / 4u;
 
-  Cand c{s_buf[wave], s_hist[wave], 0u, 0xffffffffull, kk};
-  uint64_t gbest = 0ull;
-  float lm = -INFINITY;
-  float lz = 0.0f;
-  bool first = true;
+  WaveState st{{0ull, 0xffffffffull, s_buf[wave], 0u, kk}, 0ull, -INFINITY, 0.0f, true};
 
-  for (uint32_t base = wbegin; base < wend; base += kWave * 4 * kStepVec) {
-    float v[kStepVec][4];
-    uint32_t cnt[kStepVec][4];
+  if (q_end > q_begin) {
+    // Double-buffered: step s+1 is loaded (addresses clamped into the slice)
+    // before step s is processed, so loads stay in flight.
+    f4 xa[kStepVec], xb[kStepVec];
+    u4 ya[kStepVec], yb[kStepVec];
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++) {
-      const uint32_t idx = base + (j * kWave + lane) * 4u;
-      if (kVec && idx + 3u < wend) {
-        const f4 x = __builtin_nontemporal_load(reinterpret_cast<const f4*>(lrow + idx));
-        v[j][0] = x.x; v[j][1] = x.y; v[j][2] = x.z; v[j][3] = x.w;
-        if (pen) {
-          const u4 y = __builtin_nontemporal_load(reinterpret_cast<const u4*>(crow + idx));
-          cnt[j][0] = y.x; cnt[j][1] = y.y; cnt[j][2] = y.z; cnt[j][3] = y.w;
-        } else {
-          cnt[j][0] = cnt[j][1] = cnt[j][2] = cnt[j][3] = 0u;
-        }
-      } else {
+    for (int j = 0; j < kStepVec; j++)
+      load_quad<kVec>(lrow, crow, pen, min(q_begin + j * kWave + lane, q_end - 1u), xa[j], ya[j]);
+    for (uint32_t q0 = q_begin; q0 < q_end; q0 += kStepQuads) {
+      const uint32_t qn = q0 + kStepQuads;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const uint32_t i = idx + e;
-          const bool ok = i < wend;
-          v[j][e] = ok ? lrow[i] : -INFINITY;
-          cnt[j][e] = (pen && ok) ? crow[i] : 0u;
-        }
+      for (int j = 0; j < kStepVec; j++)
+        load_quad<kVec>(lrow, crow, pen, min(qn + j * kWave + lane, q_end - 1u), xb[j], yb[j]);
+      process_step(st, p, pen, greedy, L, log2e_over_t, prow, xa, ya, q0, q_end);
+#pragma unroll
+      for (int j = 0; j < kStepVec; j++) {
+        xa[j] = xb[j];
+        ya[j] = yb[j];
       }
     }
-    // Penalties, write-back (verification only), greedy and log-sum-exp.
-    float step_max = -INFINITY;
-    uint32_t lane_max_key = 0u;
-#pragma unroll
-    for (int j = 0; j < kStepVec; j++) {
-      const uint32_t idx = base + (j * kWave + lane) * 4u;
+  }
+  {
+    // Fewer than 4 trailing elements (only at the end of a row): lane 0.
+    const uint32_t tail = (wend - wbegin) & 3u;
+    if (tail) {
+      const uint32_t i0 = q_end * 4u;
+      float v[4];
+      uint32_t cc[4];
+      bool valid[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const uint32_t i = idx + e;
-        const bool ok = i < wend;
-        if (pen) v[j][e] = penalise(v[j][e], cnt[j][e], p.presence, p.frequency, p.repetition);
-        if (prow && ok) prow[i] = v[j][e];
+        valid[e] = lane == 0u && static_cast<uint32_t>(e) < tail;
+        v[e] = valid[e] ? lrow[i0 + e] : -INFINITY;
+        cc[e] = (valid[e] && pen) ? crow[i0 + e] : 0u;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        if (pen && valid[e]) v[e] = penalise(v[e], cc[e], p.presence, p.frequency, p.repetition);
+        if (prow && valid[e]) prow[i0 + e] = v[e];
+        const uint32_t key = valid[e] ? float_key(v[e]) : 0u;
         if (greedy) {
-          const uint64_t g = greedy_comp(v[j][e], ok ? i : kInvalidId);
-          gbest = g > gbest ? g : gbest;
+          const uint64_t g = greedy_comp(v[e], valid[e] ? i0 + e : kInvalidId);
+          st.gbest = g > st.gbest ? g : st.gbest;
         }
-        const uint32_t key = ok ? float_key(v[j][e]) : 0u;
-        if (key) {
-          step_max = fmaxf(step_max, v[j][e]);
-          lane_max_key = key > lane_max_key ? key : lane_max_key;
+        if (L && key) {
+          if (v[e] > st.lm) {
+            st.lz = (st.lm == -INFINITY) ? 0.0f : st.lz * exp2f((st.lm - v[e]) * log2e_over_t);
+            st.lm = v[e];
+          }
+          st.lz += exp2f((v[e] - st.lm) * log2e_over_t);
         }
-      }
-    }
-    if (L) {
-      if (step_max > lm) {
-        lz = (lm == -INFINITY) ? 0.0f : lz * exp2f((lm - step_max) * log2e_over_t);
-        lm = step_max;
-      }
-#pragma unroll
-      for (int j = 0; j < kStepVec; j++) {
-        const uint32_t idx = base + (j * kWave + lane) * 4u;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const bool ok = idx + e < wend;
-          if (ok && is_finite_bits(__float_as_uint(v[j][e])))
-            lz += exp2f((v[j][e] - lm) * log2e_over_t);
-        }
-      }
-    }
-    if (kk) {
-      if (first) {
-        // The kk-th largest lane maximum: at least kk keys of this step are
-        // >= it, so it bounds the wave's kk-th key from below.
-        const uint32_t sorted = wave_sort_desc_u32(lane_max_key);
-        const uint32_t T = __shfl(sorted, static_cast<int>(kk - 1u));
-        const uint64_t R = T ? ((static_cast<uint64_t>(T) << 32) - 1ull) : 0xffffffffull;
-        if (R > c.R) c.R = R;
-        first = false;
-      }
-#pragma unroll
-      for (int j = 0; j < kStepVec; j++) {
-        const uint32_t idx = base + (j * kWave + lane) * 4u;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const uint32_t i = idx + e;
-          const uint32_t key = i < wend ? float_key(v[j][e]) : 0u;
-          cand_push(c, make_comp(key, i));
-        }
+        if (kk) top_stage(st.t, make_comp(key, i0 + e));
       }
     }
   }
 
-  // ---- workgroup merge ----
-  if (kk) cand_reduce(c);
-  if (lane == 0) s_n[wave] = c.n;
-  if (greedy) {
-    gbest = wave_max_u64(gbest);
-    if (lane == 0) s_greedy[wave] = gbest;
-  }
-  if (L) {
-    const double wm = wave_max_f64(static_cast<double>(lm));
-    const double lzd = (lm == -INFINITY) ? 0.0
-        : static_cast<double>(lz) * exp((static_cast<double>(lm) - wm) / t_eff);
-    const double wz = wave_sum_f64(lzd);
-    if (lane == 0) { s_lm[wave] = wm; s_lz[wave] = wz; }
-  }
-  __syncthreads();
+  // ---- per-wave results ----
+  if (kk) top_drain(st.t, true);
+  const uint64_t mine = (kk && lane < kk) ? st.t.top : 0ull;
+  const uint64_t gbest = greedy ? wave_max_u64(st.gbest) : 0ull;
+  double wm = -INFINITY, wz = 0.0;
+  if (L) wave_lse_combine(static_cast<double>(st.lm), static_cast<double>(st.lz), t_eff, &wm, &wz);
 
-  const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
-  if (wave == 0) {
-    if (kk) {
-      uint32_t n = 0;
-      const uint64_t mine = wave0_merge(s_buf, s_n, s_hist[0], kk, &n);
-      a.cand[slot * kMaxK + lane] = mine;
-      if (n == kk) {
-        const uint64_t kth = __shfl(mine, static_cast<int>(kk - 1u));
-        if (lane == 0) atomicMax(&a.row_thr[row], comp_key(kth));
-      }
-    }
+  uint64_t fin = 0ull;
+  uint64_t g = 0ull;
+  double m = -INFINITY, z = 0.0;
+  if (a.chunks == 1u) {
+    // The whole row is in this workgroup: merge from LDS.
+    if (kk) s_top[wave][lane] = mine;
     if (lane == 0) {
-      if (greedy) {
-        uint64_t g = s_greedy[0];
-        for (int w = 1; w < kWaves; w++) g = s_greedy[w] > g ? s_greedy[w] : g;
-        a.greedy[slot] = g;
-      }
-      if (L) {
-        double m = s_lm[0];
-        for (int w = 1; w < kWaves; w++) m = s_lm[w] > m ? s_lm[w] : m;
-        double z = 0.0;
-        if (m != -INFINITY)
-          for (int w = 0; w < kWaves; w++)
-            if (s_lm[w] != -INFINITY) z += s_lz[w] * exp((s_lm[w] - m) / t_eff);
-        a.lse[slot * 2] = m;
-        a.lse[slot * 2 + 1] = z;
-      }
+      s_greedy[wave] = gbest;
+      s_lm[wave] = wm;
+      s_lz[wave] = wz;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    if (kk) {
+      fin = mine;
+      for (int w = 1; w < kWaves; w++) fin = wave_merge_desc(fin, s_top[w][lane]);
+    }
+    for (int w = 0; w < kWaves; w++) {
+      g = s_greedy[w] > g ? s_greedy[w] : g;
+      m = s_lm[w] > m ? s_lm[w] : m;
+    }
+    if (L && m != -INFINITY)
+      for (int w = 0; w < kWaves; w++)
+        if (s_lm[w] != -INFINITY) z += s_lz[w] * exp((s_lm[w] - m) / t_eff);
+    finish_row(a, p, row, fin, g, m, z, lrow, crow, pen);
+    return;
+  }
+
+  // Publish this wave's partials with device-coherent stores.
+  const uint64_t slot = (static_cast<uint64_t>(row) * a.chunks + chunk) * kWaves + wave;
+  if (kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, mine);
+  if (lane == 0) {
+    if (greedy) store_coherent(a.greedy + slot, gbest);
+    if (L) {
+      store_coherent_f64(a.lse + slot * 2, wm);
+      store_coherent_f64(a.lse + slot * 2 + 1, wz);
     }
   }
-  __threadfence();
+  wait_memory();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = atomicAdd(&a.row_done[row], 1u);
-    s_last = (old == a.chunks - 1u);
-  }
+  if (threadIdx.x == 0)
+    s_last = atomicAdd(&a.row_done[row * kLineWords], 1u) == a.chunks - 1u;
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
 
-  // ---- last workgroup of the row: merge the row ----
-  const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
-  uint64_t fin = 0ull;   // wave 0: lane i holds the i-th best composite (key order)
-  uint32_t fin_n = 0;
+  // ---- last workgroup of the row: merge the row's sorted wave lists ----
+  const uint32_t lists = a.chunks * kWaves;
+  const uint64_t row_slot = static_cast<uint64_t>(row) * lists;
   if (kk) {
-    const uint32_t thr = __hip_atomic_load(&a.row_thr[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    Cand m{s_buf[wave], s_hist[wave], 0u,
-           thr ? ((static_cast<uint64_t>(thr) << 32) - 1ull) : 0xffffffffull, kk};
-    for (uint32_t ch = wave; ch < a.chunks; ch += kWaves) {
-      const uint64_t* list = a.cand + (row_slot + ch) * kMaxK;
-      const uint64_t x = lane < kk
-          ? __hip_atomic_load(list + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-      cand_push(m, x);
+    uint64_t acc = 0ull;
+    // Wave w merges lists w, w+4, ...; loads go out in groups of 8.
+    for (uint32_t l0 = wave; l0 < lists; l0 += 8u * kWaves) {
+      uint64_t x[8];
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const uint32_t li = l0 + t * kWaves;
+        x[t] = (li < lists && lane < kk) ? load_coherent(a.cand + (row_slot + li) * kMaxK + lane)
+                                         : 0ull;
+      }
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        // A list whose best entry cannot enter the running top-kk is skipped.
+        const uint64_t kth = readlane64(acc, kk - 1u);
+        if (readlane64(x[t], 0) > kth) acc = wave_merge_desc(acc, x[t]);
+      }
     }
-    cand_reduce(m);
-    if (lane == 0) s_n[wave] = m.n;
+    s_top[wave][lane] = acc;
     __syncthreads();
-    if (wave == 0) fin = wave0_merge(s_buf, s_n, s_hist[0], kk, &fin_n);
+    if (wave == 0) {
+      fin = acc;
+      for (int w = 1; w < kWaves; w++) fin = wave_merge_desc(fin, s_top[w][lane]);
+    }
   }
   if (wave != 0) return;
-
-  int32_t status = kStOk;
-  uint32_t token = kInvalidId;
-  float token_logit = -INFINITY;
-
   if (greedy) {
-    const uint64_t g = lane < a.chunks
-        ? __hip_atomic_load(a.greedy + row_slot + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-        : 0ull;
-    const uint64_t best = wave_max_u64(g);
-    const uint32_t id = comp_id(best);
-    float v = -INFINITY;
-    if (best != 0ull && id < a.vocab) {
-      v = lrow[id];
-      if (pen) v = penalise(v, crow[id], p.presence, p.frequency, p.repetition);
+    for (uint32_t i = lane; i < lists; i += kWave) {
+      const uint64_t x = load_coherent(a.greedy + row_slot + i);
+      g = x > g ? x : g;
     }
-    if (best == 0ull || !is_finite_bits(__float_as_uint(v))) {
-      status = pen ? kStFormat : kStMismatch;
-      token_logit = v;
-    } else {
-      token = id;
-      token_logit = v;
-    }
-  } else {
-    // fg_sampler_select (src/sampler.c:80-122) over the exact top_k, in value
-    // order, with parallel prefix sums in f64.
-    const uint32_t topk = p.top_k;
-    const uint64_t sel_comp = value_comp_from(lane < topk ? fin : 0ull);
-    const uint64_t sorted = wave_sort_desc_u64(sel_comp);
-    const uint32_t kept = static_cast<uint32_t>(__popcll(ballot(sorted != 0ull)));
-    if (kept == 0u) {
-      status = kStFormat;
-    } else {
-      const uint32_t limit = topk < kept ? topk : kept;
-      const bool live = lane < limit;
-      const float vf = live ? key_to_float(comp_key(sorted)) : 0.0f;
-      const double v = static_cast<double>(vf);
-      const double vmax = __shfl(v, 0);
-      const double e = live ? exp(v - vmax) : 0.0;
-      const double esum_inc = wave_prefix_sum_f64(e);
-      const double sum = __shfl(esum_inc, static_cast<int>(limit - 1u));
-      if (!(sum > 0.0) || !isfinite(sum)) {
-        status = kStFormat;
-      } else {
-        const double q = e / sum;
-        const double cum = wave_prefix_sum_f64(q);
-        const uint64_t hit = ballot(live && cum >= static_cast<double>(p.top_p));
-        const uint32_t cutoff = hit ? static_cast<uint32_t>(__builtin_ctzll(hit)) + 1u : limit;
-        const double t = static_cast<double>(p.temperature);
-        const double vmax_t = vmax / t;
-        const double te = lane < cutoff ? exp(v / t - vmax_t) : 0.0;
-        const double tcum = wave_prefix_sum_f64(te);
-        const double tsum = __shfl(tcum, static_cast<int>(cutoff - 1u));
-        if (!(tsum > 0.0) || !isfinite(tsum)) {
-          status = kStFormat;
-        } else {
-          float u = a.uniforms[row];
-          if (!is_finite_bits(__float_as_uint(u)) || u < 0.0f) u = 0.0f;
-          if (u >= 1.0f) u = __uint_as_float(0x3f7fffffu);
-          const double draw = static_cast<double>(u) * tsum;
-          const uint64_t hit2 = ballot(lane < cutoff && draw < tcum);
-          const uint32_t pick = hit2 ? static_cast<uint32_t>(__builtin_ctzll(hit2)) : cutoff - 1u;
-          const uint64_t chosen = __shfl(sorted, static_cast<int>(pick));
-          token = comp_id(chosen);
-          // The logit keeps its sign of zero: take it from the key-order list.
-          const uint64_t owner = ballot(fin != 0ull && comp_id(fin) == token);
-          const uint64_t orig = __shfl(fin, static_cast<int>(__builtin_ctzll(owner)));
-          token_logit = key_to_float(comp_key(orig));
-        }
-      }
-    }
+    g = wave_max_u64(g);
   }
-
   if (L) {
-    // Log-probs of the first L of the kk candidates in value order.
-    double m = -INFINITY;
-    double z = 0.0;
-    const double le = lane < a.chunks ? __hip_atomic_load(a.lse + (row_slot + lane) * 2,
-                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                      : -INFINITY;
-    const double lzz = lane < a.chunks ? __hip_atomic_load(a.lse + (row_slot + lane) * 2 + 1,
-                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                       : 0.0;
-    m = wave_max_f64(le);
-    const double te = static_cast<double>(t_eff);
-    z = wave_sum_f64(le == -INFINITY ? 0.0 : lzz * exp((le - m) / te));
-    const double lse = m / te + log(z);
-    const uint64_t vs = wave_sort_desc_u64(value_comp_from(fin));
-    if (lane < L) {
-      float lp = -INFINITY;
-      uint32_t id = kInvalidId;
-      if (vs != 0ull) {
-        id = comp_id(vs);
-        lp = static_cast<float>(static_cast<double>(key_to_float(comp_key(vs))) / te - lse);
+    double lm = -INFINITY, lz = 0.0;
+    for (uint32_t i = lane; i < lists; i += kWave) {
+      const double mi = load_coherent_f64(a.lse + (row_slot + i) * 2);
+      const double zi = load_coherent_f64(a.lse + (row_slot + i) * 2 + 1);
+      if (mi == -INFINITY) continue;
+      if (mi > lm) {
+        lz = (lm == -INFINITY) ? 0.0 : lz * exp((lm - mi) / t_eff);
+        lm = mi;
       }
-      a.lp_values[static_cast<uint64_t>(row) * L + lane] = lp;
-      a.lp_ids[static_cast<uint64_t>(row) * L + lane] = id;
+      lz += zi * exp((mi - lm) / t_eff);
     }
+    wave_lse_combine(lm, lz, t_eff, &m, &z);
   }
-
-  if (lane == 0) {
-    a.tokens[row] = token;
-    if (a.token_logits) a.token_logits[row] = token_logit;
-    if (a.row_status) a.row_status[row] = status;
-    __hip_atomic_store(&a.row_thr[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&a.row_done[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  finish_row(a, p, row, fin, g, m, z, lrow, crow, pen);
+  if (lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
 }
 
 }  // namespace fg

@@ -50,11 +50,11 @@ struct fg_sampler_hip {
   RowParams* d_params;      // [max_rows]
   RowParams* h_params;      // host mirror of the uploaded table
   uint32_t config_rows;     // rows configured by the last set_configs
-  uint64_t* d_cand;         // [max_rows][kMaxChunks][kMaxK]
-  uint64_t* d_greedy;       // [max_rows][kMaxChunks]
-  double* d_lse;            // [max_rows][kMaxChunks][2]
-  uint32_t* d_row_thr;      // [max_rows]
-  uint32_t* d_row_done;     // [max_rows]
+  uint64_t slots;           // wave slots in the workspace
+  uint64_t* d_cand;         // [slots][kMaxK]
+  uint64_t* d_greedy;       // [slots]
+  double* d_lse;            // [slots][2]
+  uint32_t* d_row_done;     // [max_rows * kLineWords]
   uint32_t target_groups;   // workgroups per launch the chunking aims for
 };
 
@@ -158,13 +158,15 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   }
   s->vocab = vocab;
   s->max_rows = max_rows;
-  s->target_groups = 2048u;
+  s->target_groups = 512u;
   if (const char* t = getenv("FG_HIP_TARGET_GROUPS")) {
     const long v = strtol(t, nullptr, 10);
     if (v >= 1 && v <= 1 << 20) s->target_groups = static_cast<uint32_t>(v);
   }
   hipError_t e = hipGetDevice(&s->device);
-  const uint64_t slots = static_cast<uint64_t>(max_rows) * fg::kMaxChunks;
+  // rows * chunks(rows) <= target_groups + rows for every batch size.
+  const uint64_t slots = (static_cast<uint64_t>(s->target_groups) + max_rows) * fg::kWaves;
+  s->slots = slots;
   s->h_params = static_cast<RowParams*>(calloc(max_rows, sizeof(RowParams)));
   if (!s->h_params) {
     free(s);
@@ -175,10 +177,9 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMalloc(&s->d_cand, sizeof(uint64_t) * slots * fg::kMaxK);
   if (e == hipSuccess) e = hipMalloc(&s->d_greedy, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->d_lse, sizeof(double) * slots * 2);
-  if (e == hipSuccess) e = hipMalloc(&s->d_row_thr, sizeof(uint32_t) * max_rows);
-  if (e == hipSuccess) e = hipMalloc(&s->d_row_done, sizeof(uint32_t) * max_rows);
-  if (e == hipSuccess) e = hipMemset(s->d_row_thr, 0, sizeof(uint32_t) * max_rows);
-  if (e == hipSuccess) e = hipMemset(s->d_row_done, 0, sizeof(uint32_t) * max_rows);
+  const size_t done_bytes = sizeof(uint32_t) * fg::kLineWords * max_rows;
+  if (e == hipSuccess) e = hipMalloc(&s->d_row_done, done_bytes);
+  if (e == hipSuccess) e = hipMemset(s->d_row_done, 0, done_bytes);
   if (e == hipSuccess) e = hipMemset(s->d_params, 0, sizeof(RowParams) * max_rows);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
@@ -195,7 +196,6 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   (void)hipFree(s->d_cand);
   (void)hipFree(s->d_greedy);
   (void)hipFree(s->d_lse);
-  (void)hipFree(s->d_row_thr);
   (void)hipFree(s->d_row_done);
   free(s->h_params);
   free(s);
@@ -258,6 +258,10 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
   if (wave_elems < 4u) wave_elems = 4u;
   chunks = (vocab + wave_elems * fg::kWaves - 1u) / (wave_elems * fg::kWaves);
 
+  if (static_cast<uint64_t>(b->rows) * chunks * fg::kWaves > s->slots) {
+    fg_error_set(err, FG_ERR_LIMIT, "sampler workspace too small for %u rows", b->rows);
+    return FG_ERR_LIMIT;
+  }
   fg::SampleArgs a{};
   a.logits = b->logits;
   a.lstride = b->logits_stride;
@@ -279,7 +283,6 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
   a.cand = s->d_cand;
   a.greedy = s->d_greedy;
   a.lse = s->d_lse;
-  a.row_thr = s->d_row_thr;
   a.row_done = s->d_row_done;
 
   const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
