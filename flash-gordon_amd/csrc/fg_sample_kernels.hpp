@@ -80,7 +80,23 @@ struct SampleArgs {
   double* lse;           // [slot][2] (max s, sum exp((s - max)/T))
   uint32_t* row_done;    // [rows * kLineWords] arrivals, one cache line per row,
                          // reset by the last workgroup
+  uint64_t* trace;       // FG_SAMPLE_TRACE builds only: [workgroup][8] timestamps
 };
+
+// Phase timestamps (s_memrealtime, 100 MHz) for builds with FG_SAMPLE_TRACE;
+// compiled out otherwise.
+#ifdef FG_SAMPLE_TRACE
+#define FG_TRACE(a, slot)                                                          \
+  do {                                                                             \
+    if (threadIdx.x == 0 && (a).trace)                                             \
+      (a).trace[static_cast<uint64_t>(blockIdx.x) * 8u + (slot)] =                 \
+          __builtin_amdgcn_s_memrealtime();                                        \
+  } while (0)
+#else
+#define FG_TRACE(a, slot) \
+  do {                    \
+  } while (0)
+#endif
 
 // Device-coherent (sc1) accesses for the cross-workgroup hand-off.
 template <typename T>
@@ -121,12 +137,23 @@ struct TopList {
   uint64_t* buf;   // kCap staged composites (wave-private LDS)
   uint32_t n;      // staged entries (wave-uniform)
   uint32_t kk;     // entries of the list that matter (1..64)
+  float fM;        // float form of R for elements later in the stream
 };
+
+// Raises R.  For an element later in the stream than every list member, a
+// key above comp_key(R) is needed (a tie on the key loses on the id), so the
+// stream filter is v >= fM with fM the float of key comp_key(R) + 1; it may
+// let a few extra values through (-0 against +0), never too few.
+__device__ __forceinline__ void top_raise(TopList& t, uint64_t R) {
+  if (R <= t.R) return;
+  t.R = R;
+  const uint32_t m = comp_key(R) + 1u;
+  t.fM = m < 0x00800000u ? -3.402823466e38f : key_to_float(m);
+}
 
 __device__ __forceinline__ void top_merge_sorted(TopList& t, uint64_t sorted_desc) {
   t.top = wave_merge_desc(t.top, sorted_desc);
-  const uint64_t kth = readlane64(t.top, t.kk - 1u);
-  if (kth > t.R) t.R = kth;
+  top_raise(t, readlane64(t.top, t.kk - 1u));
 }
 
 // Moves staged entries into the list: whole groups of 64, or everything when
@@ -151,6 +178,16 @@ __device__ __forceinline__ void top_stage(TopList& t, uint64_t comp) {
   const uint64_t m = ballot(pass);
   if (m == 0ull) return;
   if (pass) t.buf[t.n + lanes_below(m)] = comp;
+  t.n += static_cast<uint32_t>(__popcll(m));
+}
+
+// Stream form: stages value v (element `id`, later in the stream than every
+// list member) when it passes the float filter.
+__device__ __forceinline__ void top_stage_stream(TopList& t, bool valid, float v, uint32_t id) {
+  const bool pass = valid && v >= t.fM && v < INFINITY;
+  const uint64_t m = ballot(pass);
+  if (m == 0ull) return;
+  if (pass) t.buf[t.n + lanes_below(m)] = make_comp(float_key(v), id);
   t.n += static_cast<uint32_t>(__popcll(m));
 }
 
@@ -282,6 +319,17 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
 
 // ---- streaming ---------------------------------------------------------------
 
+// Which parts of the pass a launch needs (the union over its rows).  Each
+// combination is its own instantiation, so a launch carries only its code.
+template <bool kVec_, bool kPen_, bool kGreedy_, bool kTop_, bool kLse_>
+struct Features {
+  static constexpr bool kVec = kVec_;      // 16-byte aligned rows: vector loads
+  static constexpr bool kPen = kPen_;      // some row applies penalties
+  static constexpr bool kGreedy = kGreedy_;  // some row is greedy
+  static constexpr bool kTop = kTop_;      // some row keeps a top list
+  static constexpr bool kLse = kLse_;      // log-probs requested
+};
+
 template <bool kVec>
 __device__ __forceinline__ void load_quad(const float* lrow, const uint32_t* crow, bool pen,
                                           uint32_t q, f4& x, u4& y) {
@@ -298,16 +346,46 @@ __device__ __forceinline__ void load_quad(const float* lrow, const uint32_t* cro
 
 struct WaveState {
   TopList t;
-  uint64_t gbest;
-  float lm;  // per-lane max of finite s
-  float lz;  // per-lane sum exp2((s - lm) * log2e / T)
+  float gv;      // greedy: best value seen by this lane (stream order breaks ties)
+  uint32_t gid;  // greedy: its id
+  uint32_t gnf;  // greedy: first non-finite id seen by this lane
+  float lm;      // per-lane max of finite s
+  float lz;      // per-lane sum exp2((s - lm) * log2e / T)
   bool first;
 };
 
+// Greedy update for one element in stream order (ids rise along a lane).
+__device__ __forceinline__ void greedy_stream(WaveState& st, bool valid, float v, uint32_t id) {
+  const bool bad = valid && !is_finite_bits(__float_as_uint(v));
+  st.gnf = (bad && st.gnf == kInvalidId) ? id : st.gnf;
+  const bool gt = valid && v > st.gv;
+  st.gv = gt ? v : st.gv;
+  st.gid = gt ? id : st.gid;
+}
+
+// Greedy update for an element that may come out of stream order.
+__device__ __forceinline__ void greedy_any(WaveState& st, bool valid, float v, uint32_t id) {
+  if (!valid) return;
+  if (!is_finite_bits(__float_as_uint(v))) {
+    st.gnf = id < st.gnf ? id : st.gnf;
+    return;
+  }
+  if (v > st.gv || st.gid == kInvalidId || (v == st.gv && id < st.gid)) {
+    st.gv = v;
+    st.gid = id;
+  }
+}
+
+__device__ __forceinline__ uint64_t greedy_lane_comp(const WaveState& st) {
+  if (st.gnf != kInvalidId) return (0xffffffffull << 32) | static_cast<uint64_t>(~st.gnf);
+  return st.gid != kInvalidId ? greedy_comp(st.gv, st.gid) : 0ull;
+}
+
 // One streaming step: x/y hold quads q0 + j*64 + lane (j < kStepVec); quads
 // at or past q_end are clamped duplicates and are masked out.
+template <class F>
 __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, bool pen,
-                                             bool greedy, uint32_t L, float log2e_over_t,
+                                             bool greedy, bool lse, float log2e_over_t,
                                              float* prow, const f4* x, const u4* y, uint32_t q0,
                                              uint32_t q_end) {
   const uint32_t lane = lane_id();
@@ -321,36 +399,46 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
     v[j][1] = x[j].y;
     v[j][2] = x[j].z;
     v[j][3] = x[j].w;
-    if (pen) {
-      v[j][0] = penalise(v[j][0], y[j].x, p.presence, p.frequency, p.repetition);
-      v[j][1] = penalise(v[j][1], y[j].y, p.presence, p.frequency, p.repetition);
-      v[j][2] = penalise(v[j][2], y[j].z, p.presence, p.frequency, p.repetition);
-      v[j][3] = penalise(v[j][3], y[j].w, p.presence, p.frequency, p.repetition);
-    }
-    if (prow && ok[j]) {
-#pragma unroll
-      for (int e = 0; e < 4; e++) prow[q * 4u + e] = v[j][e];
-    }
   }
-  uint32_t lane_max_key = 0u;
-  float step_max = -INFINITY;
+  if (F::kPen && pen) {
+    // Penalties touch only elements with a nonzero count (sparse): a 64-lane
+    // slot pays for the IEEE division only when one of its lanes needs it.
 #pragma unroll
-  for (int j = 0; j < kStepVec; j++) {
-    const uint32_t q = q0 + j * kWave + lane;
+    for (int j = 0; j < kStepVec; j++) {
+      const uint32_t c4[4] = {y[j].x, y[j].y, y[j].z, y[j].w};
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
-      if (greedy) {
-        const uint64_t g = greedy_comp(v[j][e], ok[j] ? q * 4u + e : kInvalidId);
-        st.gbest = g > st.gbest ? g : st.gbest;
-      }
-      if (key) {
-        lane_max_key = key > lane_max_key ? key : lane_max_key;
-        step_max = fmaxf(step_max, v[j][e]);
+      for (int e = 0; e < 4; e++) {
+        const bool nz = c4[e] != 0u;
+        if (ballot(nz) != 0ull) {
+          if (nz) v[j][e] = penalise(v[j][e], c4[e], p.presence, p.frequency, p.repetition);
+        }
       }
     }
   }
-  if (L) {
+  if (prow) {
+#pragma unroll
+    for (int j = 0; j < kStepVec; j++)
+      if (ok[j]) {
+        const uint32_t q = q0 + j * kWave + lane;
+#pragma unroll
+        for (int e = 0; e < 4; e++) prow[q * 4u + e] = v[j][e];
+      }
+  }
+  if (F::kGreedy && greedy) {
+#pragma unroll
+    for (int j = 0; j < kStepVec; j++) {
+      const uint32_t q = q0 + j * kWave + lane;
+#pragma unroll
+      for (int e = 0; e < 4; e++) greedy_stream(st, ok[j], v[j][e], q * 4u + e);
+    }
+  }
+  if (F::kLse && lse) {
+    float step_max = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kStepVec; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (ok[j] && is_finite_bits(__float_as_uint(v[j][e]))) step_max = fmaxf(step_max, v[j][e]);
     if (step_max > st.lm) {
       st.lz = (st.lm == -INFINITY) ? 0.0f : st.lz * exp2f((st.lm - step_max) * log2e_over_t);
       st.lm = step_max;
@@ -362,24 +450,27 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
         if (ok[j] && is_finite_bits(__float_as_uint(v[j][e])))
           st.lz += exp2f((v[j][e] - st.lm) * log2e_over_t);
   }
-  if (st.t.kk) {
+  if (F::kTop && st.t.kk) {
     if (st.first) {
       // The kk-th largest lane maximum: at least kk keys of this step are >=
       // it, so it bounds the wave's kk-th key from below.
-      const uint32_t sorted = wave_sort_desc_u32(lane_max_key);
-      const uint32_t T = readlane32(sorted, st.t.kk - 1u);
-      const uint64_t R = T ? ((static_cast<uint64_t>(T) << 32) - 1ull) : 0xffffffffull;
-      if (R > st.t.R) st.t.R = R;
+      uint32_t lane_max_key = 0u;
+#pragma unroll
+      for (int j = 0; j < kStepVec; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
+          lane_max_key = key > lane_max_key ? key : lane_max_key;
+        }
+      const uint32_t T = readlane32(wave_sort_desc_u32(lane_max_key), st.t.kk - 1u);
+      if (T) top_raise(st.t, (static_cast<uint64_t>(T) << 32) - 1ull);
       st.first = false;
     }
 #pragma unroll
     for (int j = 0; j < kStepVec; j++) {
       const uint32_t q = q0 + j * kWave + lane;
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
-        top_stage(st.t, make_comp(key, q * 4u + e));
-      }
+      for (int e = 0; e < 4; e++) top_stage_stream(st.t, ok[j], v[j][e], q * 4u + e);
     }
     top_drain(st.t, false);
   }
@@ -387,9 +478,9 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
 
 // ---- the fused kernel ------------------------------------------------------
 
-template <bool kVec>
+template <class F>
 __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
-  __shared__ uint64_t s_buf[kWaves][kCap];
+  __shared__ uint64_t s_buf[F::kTop ? kWaves : 1][F::kTop ? kCap : 1];
   __shared__ uint64_t s_top[kWaves][kWave];
   __shared__ uint64_t s_greedy[kWaves];
   __shared__ double s_lm[kWaves];
@@ -403,6 +494,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const RowParams p = a.params[row];
   const bool greedy = p.temperature == 0.0f;
   const uint32_t L = a.logprobs;
+  const bool lse = F::kLse && L != 0u;
   const uint32_t kk = greedy ? L : (p.top_k > L ? p.top_k : L);
   const bool pen = (p.flags & kRowPenalties) && a.counts != nullptr;
   const float t_eff = p.temperature > 0.0f ? p.temperature : 1.0f;
@@ -417,7 +509,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint32_t q_begin = wbegin / 4u;
   const uint32_t q_end = (wbegin + ((wend - wbegin) & ~3u)) / 4u;
 
-  WaveState st{{0ull, 0xffffffffull, s_buf[wave], 0u, kk}, 0ull, -INFINITY, 0.0f, true};
+  WaveState st{{0ull, 0xffffffffull, F::kTop ? s_buf[wave] : nullptr, 0u, F::kTop ? kk : 0u,
+                -3.402823466e38f},
+               -INFINITY, kInvalidId, kInvalidId, -INFINITY, 0.0f, true};
+  FG_TRACE(a, 0);
 
   if (q_end > q_begin) {
     // Double-buffered: step s+1 is loaded (addresses clamped into the slice)
@@ -426,13 +521,15 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     u4 ya[kStepVec], yb[kStepVec];
 #pragma unroll
     for (int j = 0; j < kStepVec; j++)
-      load_quad<kVec>(lrow, crow, pen, min(q_begin + j * kWave + lane, q_end - 1u), xa[j], ya[j]);
+      load_quad<F::kVec>(lrow, crow, F::kPen && pen, min(q_begin + j * kWave + lane, q_end - 1u),
+                         xa[j], ya[j]);
     for (uint32_t q0 = q_begin; q0 < q_end; q0 += kStepQuads) {
       const uint32_t qn = q0 + kStepQuads;
 #pragma unroll
       for (int j = 0; j < kStepVec; j++)
-        load_quad<kVec>(lrow, crow, pen, min(qn + j * kWave + lane, q_end - 1u), xb[j], yb[j]);
-      process_step(st, p, pen, greedy, L, log2e_over_t, prow, xa, ya, q0, q_end);
+        load_quad<F::kVec>(lrow, crow, F::kPen && pen, min(qn + j * kWave + lane, q_end - 1u),
+                           xb[j], yb[j]);
+      process_step<F>(st, p, pen, greedy, lse, log2e_over_t, prow, xa, ya, q0, q_end);
 #pragma unroll
       for (int j = 0; j < kStepVec; j++) {
         xa[j] = xb[j];
@@ -445,49 +542,41 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     const uint32_t tail = (wend - wbegin) & 3u;
     if (tail) {
       const uint32_t i0 = q_end * 4u;
-      float v[4];
-      uint32_t cc[4];
-      bool valid[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        valid[e] = lane == 0u && static_cast<uint32_t>(e) < tail;
-        v[e] = valid[e] ? lrow[i0 + e] : -INFINITY;
-        cc[e] = (valid[e] && pen) ? crow[i0 + e] : 0u;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        if (pen && valid[e]) v[e] = penalise(v[e], cc[e], p.presence, p.frequency, p.repetition);
-        if (prow && valid[e]) prow[i0 + e] = v[e];
-        const uint32_t key = valid[e] ? float_key(v[e]) : 0u;
-        if (greedy) {
-          const uint64_t g = greedy_comp(v[e], valid[e] ? i0 + e : kInvalidId);
-          st.gbest = g > st.gbest ? g : st.gbest;
-        }
-        if (L && key) {
-          if (v[e] > st.lm) {
-            st.lz = (st.lm == -INFINITY) ? 0.0f : st.lz * exp2f((st.lm - v[e]) * log2e_over_t);
-            st.lm = v[e];
+        const bool valid = lane == 0u && static_cast<uint32_t>(e) < tail;
+        float v = valid ? lrow[i0 + e] : -INFINITY;
+        const uint32_t c = (valid && pen) ? crow[i0 + e] : 0u;
+        if (pen && valid) v = penalise(v, c, p.presence, p.frequency, p.repetition);
+        if (prow && valid) prow[i0 + e] = v;
+        if (F::kGreedy && greedy) greedy_stream(st, valid, v, i0 + e);
+        if (lse && valid && is_finite_bits(__float_as_uint(v))) {
+          if (v > st.lm) {
+            st.lz = (st.lm == -INFINITY) ? 0.0f : st.lz * exp2f((st.lm - v) * log2e_over_t);
+            st.lm = v;
           }
-          st.lz += exp2f((v[e] - st.lm) * log2e_over_t);
+          st.lz += exp2f((v - st.lm) * log2e_over_t);
         }
-        if (kk) top_stage(st.t, make_comp(key, i0 + e));
+        if (F::kTop && kk) top_stage(st.t, make_comp(valid ? float_key(v) : 0u, i0 + e));
       }
     }
   }
 
   // ---- per-wave results ----
-  if (kk) top_drain(st.t, true);
-  const uint64_t mine = (kk && lane < kk) ? st.t.top : 0ull;
-  const uint64_t gbest = greedy ? wave_max_u64(st.gbest) : 0ull;
+  FG_TRACE(a, 1);
+  if (F::kTop && kk) top_drain(st.t, true);
+  FG_TRACE(a, 2);
+  const uint64_t mine = (F::kTop && kk && lane < kk) ? st.t.top : 0ull;
+  const uint64_t gbest = (F::kGreedy && greedy) ? wave_max_u64(greedy_lane_comp(st)) : 0ull;
   double wm = -INFINITY, wz = 0.0;
-  if (L) wave_lse_combine(static_cast<double>(st.lm), static_cast<double>(st.lz), t_eff, &wm, &wz);
+  if (lse) wave_lse_combine(static_cast<double>(st.lm), static_cast<double>(st.lz), t_eff, &wm, &wz);
 
   uint64_t fin = 0ull;
   uint64_t g = 0ull;
   double m = -INFINITY, z = 0.0;
   if (a.chunks == 1u) {
     // The whole row is in this workgroup: merge from LDS.
-    if (kk) s_top[wave][lane] = mine;
+    if (F::kTop) s_top[wave][lane] = mine;
     if (lane == 0) {
       s_greedy[wave] = gbest;
       s_lm[wave] = wm;
@@ -495,7 +584,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     }
     __syncthreads();
     if (wave != 0) return;
-    if (kk) {
+    if (F::kTop && kk) {
       fin = mine;
       for (int w = 1; w < kWaves; w++) fin = wave_merge_desc(fin, s_top[w][lane]);
     }
@@ -503,7 +592,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       g = s_greedy[w] > g ? s_greedy[w] : g;
       m = s_lm[w] > m ? s_lm[w] : m;
     }
-    if (L && m != -INFINITY)
+    if (lse && m != -INFINITY)
       for (int w = 0; w < kWaves; w++)
         if (s_lm[w] != -INFINITY) z += s_lz[w] * exp((s_lm[w] - m) / t_eff);
     finish_row(a, p, row, fin, g, m, z, lrow, crow, pen);
@@ -512,25 +601,27 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
 
   // Publish this wave's partials with device-coherent stores.
   const uint64_t slot = (static_cast<uint64_t>(row) * a.chunks + chunk) * kWaves + wave;
-  if (kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, mine);
+  if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, mine);
   if (lane == 0) {
-    if (greedy) store_coherent(a.greedy + slot, gbest);
-    if (L) {
+    if (F::kGreedy && greedy) store_coherent(a.greedy + slot, gbest);
+    if (lse) {
       store_coherent_f64(a.lse + slot * 2, wm);
       store_coherent_f64(a.lse + slot * 2 + 1, wz);
     }
   }
   wait_memory();
   __syncthreads();
+  FG_TRACE(a, 3);
   if (threadIdx.x == 0)
     s_last = atomicAdd(&a.row_done[row * kLineWords], 1u) == a.chunks - 1u;
   __syncthreads();
+  FG_TRACE(a, 4);
   if (!s_last) return;
 
   // ---- last workgroup of the row: merge the row's sorted wave lists ----
   const uint32_t lists = a.chunks * kWaves;
   const uint64_t row_slot = static_cast<uint64_t>(row) * lists;
-  if (kk) {
+  if (F::kTop && kk) {
     uint64_t acc = 0ull;
     // Wave w merges lists w, w+4, ...; loads go out in groups of 8.
     for (uint32_t l0 = wave; l0 < lists; l0 += 8u * kWaves) {
@@ -550,20 +641,21 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     }
     s_top[wave][lane] = acc;
     __syncthreads();
+    FG_TRACE(a, 5);
     if (wave == 0) {
       fin = acc;
       for (int w = 1; w < kWaves; w++) fin = wave_merge_desc(fin, s_top[w][lane]);
     }
   }
   if (wave != 0) return;
-  if (greedy) {
+  if (F::kGreedy && greedy) {
     for (uint32_t i = lane; i < lists; i += kWave) {
       const uint64_t x = load_coherent(a.greedy + row_slot + i);
       g = x > g ? x : g;
     }
     g = wave_max_u64(g);
   }
-  if (L) {
+  if (lse) {
     double lm = -INFINITY, lz = 0.0;
     for (uint32_t i = lane; i < lists; i += kWave) {
       const double mi = load_coherent_f64(a.lse + (row_slot + i) * 2);
@@ -577,8 +669,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     }
     wave_lse_combine(lm, lz, t_eff, &m, &z);
   }
+  FG_TRACE(a, 6);
   finish_row(a, p, row, fin, g, m, z, lrow, crow, pen);
   if (lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
+  FG_TRACE(a, 7);
 }
 
 }  // namespace fg

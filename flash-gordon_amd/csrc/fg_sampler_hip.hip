@@ -41,6 +41,30 @@ bool config_ok(const fg_sampler_config* c, uint32_t flags) {
   return fg_sampler_config_validate(c, nullptr) == FG_OK;
 }
 
+// One instantiation of the fused kernel per feature combination.
+using SampleLaunch = void (*)(uint32_t, hipStream_t, const fg::SampleArgs&);
+
+template <class F>
+void launch_sample(uint32_t grid, hipStream_t s, const fg::SampleArgs& a) {
+  fg::sample_rows_kernel<F><<<grid, fg::kBlock, 0, s>>>(a);
+}
+
+template <int kBits>
+constexpr SampleLaunch vec_launch() {
+  return launch_sample<fg::Features<true, (kBits & 1) != 0, (kBits & 2) != 0, (kBits & 4) != 0,
+                                    (kBits & 8) != 0>>;
+}
+
+// Indexed by pen | greedy << 1 | top << 2 | lse << 3.
+const SampleLaunch kVecLaunch[16] = {
+    vec_launch<0>(),  vec_launch<1>(),  vec_launch<2>(),  vec_launch<3>(),
+    vec_launch<4>(),  vec_launch<5>(),  vec_launch<6>(),  vec_launch<7>(),
+    vec_launch<8>(),  vec_launch<9>(),  vec_launch<10>(), vec_launch<11>(),
+    vec_launch<12>(), vec_launch<13>(), vec_launch<14>(), vec_launch<15>(),
+};
+// Rows that are not 16-byte aligned: scalar loads, every part compiled in.
+const SampleLaunch kScalarLaunch = launch_sample<fg::Features<false, true, true, true, true>>;
+
 }  // namespace
 
 struct fg_sampler_hip {
@@ -56,6 +80,7 @@ struct fg_sampler_hip {
   double* d_lse;            // [slots][2]
   uint32_t* d_row_done;     // [max_rows * kLineWords]
   uint32_t target_groups;   // workgroups per launch the chunking aims for
+  uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
 };
 
 extern "C" {
@@ -181,6 +206,10 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMalloc(&s->d_row_done, done_bytes);
   if (e == hipSuccess) e = hipMemset(s->d_row_done, 0, done_bytes);
   if (e == hipSuccess) e = hipMemset(s->d_params, 0, sizeof(RowParams) * max_rows);
+#ifdef FG_SAMPLE_TRACE
+  if (e == hipSuccess) e = hipMalloc(&s->trace, sizeof(uint64_t) * 8u * (s->target_groups + max_rows));
+  if (e == hipSuccess) e = hipMemset(s->trace, 0, sizeof(uint64_t) * 8u * (s->target_groups + max_rows));
+#endif
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     fg_sampler_hip_destroy(s);
@@ -197,6 +226,7 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   (void)hipFree(s->d_greedy);
   (void)hipFree(s->d_lse);
   (void)hipFree(s->d_row_done);
+  (void)hipFree(s->trace);
   free(s->h_params);
   free(s);
 }
@@ -284,14 +314,22 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
   a.greedy = s->d_greedy;
   a.lse = s->d_lse;
   a.row_done = s->d_row_done;
+  a.trace = s->trace;
 
   const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
                    (!b->counts || (aligned16(b->counts) && (b->counts_stride % 4u) == 0u));
+  bool any_pen = false, any_greedy = false, any_top = b->logprobs != 0u;
+  for (uint32_t r = 0; r < b->rows; r++) {
+    const RowParams& rp = s->h_params[r];
+    any_pen |= (rp.flags & fg::kRowPenalties) != 0u;
+    any_greedy |= rp.temperature == 0.0f;
+    any_top |= rp.temperature > 0.0f;
+  }
+  any_pen = any_pen && b->counts != nullptr;
+  const int bits = (any_pen ? 1 : 0) | (any_greedy ? 2 : 0) | (any_top ? 4 : 0) |
+                   (b->logprobs ? 8 : 0);
   const uint32_t grid = b->rows * chunks;
-  if (vec)
-    fg::sample_rows_kernel<true><<<grid, fg::kBlock, 0, as_stream(stream)>>>(a);
-  else
-    fg::sample_rows_kernel<false><<<grid, fg::kBlock, 0, as_stream(stream)>>>(a);
+  (vec ? kVecLaunch[bits] : kScalarLaunch)(grid, as_stream(stream), a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "sampler launch");
 }
@@ -309,5 +347,13 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "history increment launch");
 }
+
+#ifdef FG_SAMPLE_TRACE
+// Copies the last launch's phase timestamps ([workgroup][8]) to the host.
+fg_status fg_sampler_hip_trace_copy(fg_sampler_hip* s, uint64_t* host, uint64_t count) {
+  const hipError_t e = hipMemcpy(host, s->trace, sizeof(uint64_t) * count, hipMemcpyDeviceToHost);
+  return e == hipSuccess ? FG_OK : FG_ERR_UNAVAILABLE;
+}
+#endif
 
 }  // extern "C"
