@@ -2,10 +2,13 @@
 //
 // Keys: float_key is the order-preserving map of shaders/fg_topk_select.comp:27-31
 // (NaN/Inf -> 0; +0 above -0).  A candidate is carried as one 64-bit
-// "composite" (key << 32) | ~id: ids are unique within a row, so composites
-// are unique and their unsigned order is exactly the top-k order of the
-// reference's select ladder (key desc, then lower id first).  Composite 0 (and
-// anything below 2^32) means "no candidate".
+// "composite" (key << 31) | (2^31 - 1 - id), ids < 2^31: ids are unique within
+// a row, so composites are unique and their unsigned order is exactly the
+// top-k order of the reference's select ladder (key desc, then lower id
+// first).  Composite 0 (and anything below 2^31) means "no candidate".  Bit 63
+// is clear and a finite key is >= 2^23, so read as an f64 a composite is a
+// positive normal number (or +0): f64 max/min order composites in one
+// instruction each.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -53,11 +56,19 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+constexpr uint64_t kFiniteComp = 1ull << 31;  // smallest composite of a real candidate
+
 __device__ __forceinline__ uint64_t make_comp(uint32_t key, uint32_t id) {
-  return (static_cast<uint64_t>(key) << 32) | static_cast<uint64_t>(~id);
+  return (static_cast<uint64_t>(key) << 31) | static_cast<uint64_t>(0x7fffffffu - id);
 }
-__device__ __forceinline__ uint32_t comp_key(uint64_t c) { return static_cast<uint32_t>(c >> 32); }
-__device__ __forceinline__ uint32_t comp_id(uint64_t c) { return ~static_cast<uint32_t>(c); }
+__device__ __forceinline__ uint32_t comp_key(uint64_t c) { return static_cast<uint32_t>(c >> 31); }
+__device__ __forceinline__ uint32_t comp_id(uint64_t c) {
+  return 0x7fffffffu - static_cast<uint32_t>(c & 0x7fffffffull);
+}
+// The largest composite below every composite with key >= T.
+__device__ __forceinline__ uint64_t key_floor(uint32_t T) {
+  return (static_cast<uint64_t>(T) << 31) - 1ull;
+}
 
 // Greedy order of src/output.c:484-492 as one 64-bit max: non-finite values
 // rank first (hi = all ones), finite ones by key with -0 folded onto +0 (the
@@ -75,6 +86,7 @@ __device__ __forceinline__ uint64_t greedy_comp(float v, uint32_t id) {
   }
   return (static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(~id);
 }
+__device__ __forceinline__ uint32_t greedy_id(uint64_t c) { return ~static_cast<uint32_t>(c); }
 
 // Penalty of src/sampler.c:55-58 for one logit seen c > 0 times.  The kernels
 // are compiled with -ffp-contract=off so the product and the sum round
@@ -153,15 +165,21 @@ __device__ __forceinline__ uint32_t readlane32(uint32_t v, uint32_t lane) {
 // K lanes, partner at distance J; the final order is descending by lane.
 template <int K, int J, typename T>
 __device__ __forceinline__ T bitonic_step(T v) {
-  T o;
-  if constexpr (sizeof(T) == 8) o = lane_xor64<J>(v);
-  else o = lane_xor<J>(v);
   const uint32_t lane = lane_id();
   const bool desc = (K == kWave) || ((lane & K) == 0);
   const bool lower = (lane & J) == 0;
-  const T hi = o > v ? o : v;
-  const T lo = o > v ? v : o;
-  return (lower == desc) ? hi : lo;
+  if constexpr (sizeof(T) == 8) {
+    // Composites compare as f64 (see above): one max and one min.
+    const double a = __longlong_as_double(static_cast<long long>(v));
+    const double b = __longlong_as_double(static_cast<long long>(lane_xor64<J>(v)));
+    const double r = (lower == desc) ? fmax(a, b) : fmin(a, b);
+    return static_cast<T>(__double_as_longlong(r));
+  } else {
+    const T o = lane_xor<J>(v);
+    const T hi = o > v ? o : v;
+    const T lo = o > v ? v : o;
+    return (lower == desc) ? hi : lo;
+  }
 }
 
 template <int K, typename T>
@@ -192,6 +210,24 @@ __device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) { return wave
 __device__ __forceinline__ uint64_t wave_merge_desc(uint64_t a, uint64_t b) {
   const uint64_t r = lane_reverse64(b);
   return bitonic_merge_stage<64>(a > r ? a : r);
+}
+
+// Two independent merges, written side by side so their dependent chains
+// interleave.
+__device__ __forceinline__ void wave_merge_desc2(uint64_t& a0, uint64_t b0, uint64_t& a1,
+                                                 uint64_t b1) {
+  const uint64_t r0 = lane_reverse64(b0);
+  const uint64_t r1 = lane_reverse64(b1);
+  uint64_t x0 = a0 > r0 ? a0 : r0;
+  uint64_t x1 = a1 > r1 ? a1 : r1;
+  x0 = bitonic_step<64, 32>(x0); x1 = bitonic_step<64, 32>(x1);
+  x0 = bitonic_step<64, 16>(x0); x1 = bitonic_step<64, 16>(x1);
+  x0 = bitonic_step<64, 8>(x0);  x1 = bitonic_step<64, 8>(x1);
+  x0 = bitonic_step<64, 4>(x0);  x1 = bitonic_step<64, 4>(x1);
+  x0 = bitonic_step<64, 2>(x0);  x1 = bitonic_step<64, 2>(x1);
+  x0 = bitonic_step<64, 1>(x0);  x1 = bitonic_step<64, 1>(x1);
+  a0 = x0;
+  a1 = x1;
 }
 
 // ---- wave reductions and scans ------------------------------------------------

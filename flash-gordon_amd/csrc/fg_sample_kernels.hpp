@@ -197,7 +197,7 @@ __device__ __forceinline__ uint64_t value_comp_from(uint64_t key_comp) {
   if (key_comp == 0ull) return 0ull;
   uint32_t k = comp_key(key_comp);
   if (k == 0x7fffffffu) k = 0x80000000u;  // key(-0) -> key(+0)
-  return (static_cast<uint64_t>(k) << 32) | (key_comp & 0xffffffffull);
+  return (static_cast<uint64_t>(k) << 31) | (key_comp & 0x7fffffffull);
 }
 
 // A key-ordered list re-ordered by value: only -0 entries can move.
@@ -235,7 +235,7 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
 
   if (greedy) {
     // src/output.c:560-599 / 728-741: a non-finite winner is an error.
-    const uint32_t id = comp_id(gbest);
+    const uint32_t id = greedy_id(gbest);
     float v = -INFINITY;
     if (gbest != 0ull && id < a.vocab) {
       v = lrow[id];
@@ -463,7 +463,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
           lane_max_key = key > lane_max_key ? key : lane_max_key;
         }
       const uint32_t T = readlane32(wave_sort_desc_u32(lane_max_key), st.t.kk - 1u);
-      if (T) top_raise(st.t, (static_cast<uint64_t>(T) << 32) - 1ull);
+      if (T) top_raise(st.t, key_floor(T));
       st.first = false;
     }
 #pragma unroll
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint32_t q_begin = wbegin / 4u;
   const uint32_t q_end = (wbegin + ((wend - wbegin) & ~3u)) / 4u;
 
-  WaveState st{{0ull, 0xffffffffull, F::kTop ? s_buf[wave] : nullptr, 0u, F::kTop ? kk : 0u,
+  WaveState st{{0ull, kFiniteComp - 1ull, F::kTop ? s_buf[wave] : nullptr, 0u, F::kTop ? kk : 0u,
                 -3.402823466e38f},
                -INFINITY, kInvalidId, kInvalidId, -INFINITY, 0.0f, true};
   FG_TRACE(a, 0);

@@ -174,7 +174,9 @@ fg_status fg_hip_history_build(uint32_t* counts, uint64_t counts_stride, uint32_
 
 fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t max_rows,
                                 fg_error* err) {
-  if (!out || !vocab || !max_rows) return arg_fail(err, "invalid sampler dimensions");
+  // Candidate composites hold a 31-bit id.
+  if (!out || !vocab || vocab >= 0x80000000u || !max_rows)
+    return arg_fail(err, "invalid sampler dimensions");
   *out = nullptr;
   fg_sampler_hip* s = static_cast<fg_sampler_hip*>(calloc(1, sizeof *s));
   if (!s) {

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(float* out_scores, u
     for (int w = 1; w < 4; w++)
       if (s_comp[w] > best) { best = s_comp[w]; best_v = s_val[w]; }
     out_scores[blockIdx.x] = best ? best_v : -INFINITY;
-    out_ids[blockIdx.x] = best ? comp_id(best) : kInvalidId;
+    out_ids[blockIdx.x] = best ? greedy_id(best) : kInvalidId;
   }
 }
 
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void topk_select_kernel(float* out_scores, uin
   __syncthreads();
   const uint32_t take = min(limit, s_finite);
   if (wave == 0) {
-    uint64_t R = 1ull << 32;  // every finite entry
+    uint64_t R = kFiniteComp;  // every finite entry
     if (take > 0u && take < s_finite) R = wave_select_kth(s_buf, 1024u, take, s_hist);
     if (lane == 0) s_R = R;
   }
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void topk_select_kernel(float* out_scores, uin
   const uint64_t R = s_R;
   uint32_t mine = 0;
 #pragma unroll
-  for (int e = 0; e < 4; e++) mine += (take > 0u && comp[e] >= R && comp[e] >= (1ull << 32)) ? 1u : 0u;
+  for (int e = 0; e < 4; e++) mine += (take > 0u && comp[e] >= R && comp[e] >= kFiniteComp) ? 1u : 0u;
   // Exclusive prefix of `mine` over the workgroup in thread order.
   uint32_t incl = mine;
 #pragma unroll
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void topk_select_kernel(float* out_scores, uin
   const uint64_t out_base = static_cast<uint64_t>(blockIdx.x) * k;
 #pragma unroll
   for (int e = 0; e < 4; e++) {
-    if (take > 0u && comp[e] >= R && comp[e] >= (1ull << 32)) {
+    if (take > 0u && comp[e] >= R && comp[e] >= kFiniteComp) {
       const uint32_t pos = 4u * t + e;
       out_scores[out_base + off] = in_scores[base + pos];
       out_ids[out_base + off] = in_ids ? in_ids[base + pos] : base + pos;
