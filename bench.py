@@ -104,6 +104,8 @@ def main():
     ap.add_argument("--set-gb", type=float, default=4.0, help="distinct input bytes to rotate over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a 1 GiB device copy (the rocprof FETCH/WRITE_SIZE reference)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the rows of a batch are independent "
@@ -116,6 +118,17 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        # A plain copy kernel of known size: 1 GiB read + 1 GiB written per
+        # launch; its counters scale the sampler's FETCH_SIZE / WRITE_SIZE.
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": src.numel() * 4,
+                          "bytes_written": dst.numel() * 4, "launches": args.steps}))
+        return
     set_bytes = ROWS * ALG_BYTES_PER_ROW
     nsets = max(4, int(args.set_gb * 1e9 / set_bytes + 0.999))
     logits, counts, uniforms = make_sets(torch, dev, nsets)
