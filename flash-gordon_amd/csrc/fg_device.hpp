@@ -70,6 +70,80 @@ __device__ __forceinline__ uint64_t key_floor(uint32_t T) {
   return (static_cast<uint64_t>(T) << 31) - 1ull;
 }
 
+// Value-order composite: like make_comp, but -0 takes the key of +0, so two
+// zeros of either sign tie on value and the lower id ranks first (the order
+// of the select's sort, src/sampler.c:88-96).  0 for a non-finite value.
+__device__ __forceinline__ uint64_t value_comp(float v, uint32_t id) {
+  uint32_t b = __float_as_uint(v);
+  if (!is_finite_bits(b)) return 0ull;
+  if (b == 0x80000000u) b = 0u;
+  return make_comp((b & 0x80000000u) ? ~b : (b | 0x80000000u), id);
+}
+
+// e^x in f64 for x <= 0, to a few ulp, by the table-driven method of
+// P. T. P. Tang (ACM TOMS 15(2), 1989): x = (64k + j) ln2/64 + r with
+// |r| <= ln2/128 (Cody-Waite reduction with a two-part ln2/64 and fma),
+// e^x = 2^k 2^(j/64) e^r, e^r by its Taylor polynomial to r^6 (truncation
+// below 3e-20).  The table holds 2^(j/64) rounded to nearest.  Used for the
+// masses that a top-p cut compares, so that a cut agrees with an f64 libm
+// reference to ~1e-15 of the row's mass.
+__constant__ const double kExp2Frac64[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0,
+};
+
+__device__ __forceinline__ double exp_nonpos(double x) {
+  x = fmax(x, -800.0);  // e^-800 underflows to 0 like libm exp
+  const double n = rint(x * 0x1.71547652b82fep+6);  // x * 64 / ln2
+  double r = fma(-n, 0x1.62e42fefa39efp-7, x);      // x - n * ln2/64 (high part)
+  r = fma(-n, 0x1.abc9e3b39803fp-62, r);            // ... (low part)
+  double q = fma(r, 1.0 / 720.0, 1.0 / 120.0);
+  q = fma(r, q, 1.0 / 24.0);
+  q = fma(r, q, 1.0 / 6.0);
+  q = fma(r, q, 0.5);
+  q = fma(r, q, 1.0);
+  q = fma(r, q, 1.0);
+  const int ni = static_cast<int>(n);
+  return ldexp(kExp2Frac64[ni & 63] * q, ni >> 6);
+}
+
+// The same without the table: x = n ln2 + r, |r| <= ln2/2, e^r by its
+// Taylor polynomial to r^12 (truncation below 2e-16).  No memory access, for
+// use inside streaming loops.
+__device__ __forceinline__ double exp_nonpos_poly(double x) {
+  x = fmax(x, -800.0);
+  const double n = rint(x * 0x1.71547652b82fep+0);  // x / ln2
+  double r = fma(-n, 0x1.62e42fefa39efp-1, x);       // x - n ln2 (high part)
+  r = fma(-n, 0x1.abc9e3b39803fp-56, r);             // ... (low part)
+  double q = fma(r, 1.0 / 479001600.0, 1.0 / 39916800.0);
+  q = fma(r, q, 1.0 / 3628800.0);
+  q = fma(r, q, 1.0 / 362880.0);
+  q = fma(r, q, 1.0 / 40320.0);
+  q = fma(r, q, 1.0 / 5040.0);
+  q = fma(r, q, 1.0 / 720.0);
+  q = fma(r, q, 1.0 / 120.0);
+  q = fma(r, q, 1.0 / 24.0);
+  q = fma(r, q, 1.0 / 6.0);
+  q = fma(r, q, 0.5);
+  q = fma(r, q, 1.0);
+  q = fma(r, q, 1.0);
+  return ldexp(q, static_cast<int>(n));
+}
+
 // Greedy order of src/output.c:484-492 as one 64-bit max: non-finite values
 // rank first (hi = all ones), finite ones by key with -0 folded onto +0 (the
 // reference compares values, so 0 == -0 and the lower id wins), ties by lower

@@ -55,6 +55,7 @@ constexpr uint32_t kLineWords = 32;  // u32 per 128-byte cache line (row counter
 constexpr int32_t kStOk = 0;
 constexpr int32_t kStFormat = 4;
 constexpr int32_t kStMismatch = 5;
+constexpr int32_t kStLimit = 8;  // whole-row nucleus cut deeper than the kMaxK best
 
 struct SampleArgs {
   const float* logits;
@@ -78,8 +79,11 @@ struct SampleArgs {
   uint64_t* cand;        // [slot][kMaxK] top-kk composites of the wave, descending, 0 = empty
   uint64_t* greedy;      // [slot] greedy composite
   double* lse;           // [slot][2] (max s, sum exp((s - max)/T))
+  double* zsum;          // [slot][3] whole-row nucleus mass (max, sum, error bound)
   uint32_t* row_done;    // [rows * kLineWords] arrivals, one cache line per row,
                          // reset by the last workgroup
+  uint32_t* nuc_deep;    // [rows] whole-row nucleus: 1 = cut deeper than the kMaxK best
+  float* nuc_max;        // [rows] whole-row nucleus: the row's largest finite value
   uint64_t* trace;       // FG_SAMPLE_TRACE builds only: [workgroup][8] timestamps
 };
 
@@ -216,18 +220,68 @@ __device__ __forceinline__ void wave_lse_combine(double m, double z, double t, d
   *wz = wave_sum_f64(zz);
 }
 
+// Folds one (max, sum exp((s - max)/t)) partial into a running pair.
+__device__ __forceinline__ void lse_accumulate(double& m, double& z, double mi, double zi, double t) {
+  if (mi == -INFINITY) return;
+  if (mi > m) {
+    z = (m == -INFINITY) ? 0.0 : z * exp((m - mi) / t);
+    m = mi;
+  }
+  z += zi * exp((mi - m) / t);
+}
+
+// Whole-row mass for a nucleus row: (max s, z = sum exp(s - max), e = sum
+// exp(s - max) * (max - s)).  The terms are f32 exp2, each within
+// 1.2e-7 + 1.8e-7 |s - max| of exp (one ulp of v_exp_f32, plus the rounding of
+// s - max, of log2(e) and of the product), so e bounds the error of z.
+struct Mass {
+  double m, z, e;
+};
+
+// Folds (mi, zi, ei) into a running mass (rescaling the one with the lower
+// max: exp(-d) z and exp(-d) (e + d z)).
+__device__ __forceinline__ void mass_accumulate(Mass& a, double mi, double zi, double ei) {
+  if (mi == -INFINITY) return;
+  if (mi > a.m) {
+    if (a.m == -INFINITY) {
+      a.z = a.e = 0.0;
+    } else {
+      const double d = mi - a.m, f = exp(-d);
+      a.e = f * (a.e + d * a.z);
+      a.z = f * a.z;
+    }
+    a.m = mi;
+  }
+  const double d = a.m - mi, f = exp(-d);
+  a.z += f * zi;
+  a.e += f * (ei + d * zi);
+}
+
+__device__ __forceinline__ Mass wave_mass_combine(double m, double z, double e) {
+  const double mm = wave_max_f64(m);
+  double zz = 0.0, ee = 0.0;
+  if (m != -INFINITY) {
+    const double d = mm - m, f = exp(-d);
+    zz = f * z;
+    ee = f * (e + d * z);
+  }
+  return Mass{mm, wave_sum_f64(zz), wave_sum_f64(ee)};
+}
+
 // ---- the row's final step (one wave) ---------------------------------------
 
 // fin: lane i holds the row's i-th best composite in key order (0 past the
-// end); gbest: the row's greedy composite; (m, z): the row's log-sum-exp
-// partial.  Writes token, logit, status and log-probs of the row.
+// end); gbest: the row's greedy composite; (m, z): the row's tempered
+// log-sum-exp pair for log-probs; zs: the row's untempered mass for a
+// whole-row nucleus.  Writes token, logit, status and log-probs.
 __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint32_t row,
-                                  uint64_t fin, uint64_t gbest, double m, double z,
+                                  uint64_t fin, uint64_t gbest, double m, double z, Mass zs,
                                   const float* lrow, const uint32_t* crow, bool pen) {
   const uint32_t lane = lane_id();
   const bool greedy = p.temperature == 0.0f;
   const uint32_t L = a.logprobs;
-  const uint32_t kk = greedy ? L : (p.top_k > L ? p.top_k : L);
+  const bool nuc = !greedy && p.top_k == 0u;
+  const uint32_t kk = greedy ? L : nuc ? kMaxK : (p.top_k > L ? p.top_k : L);
   fin = lane < kk ? fin : 0ull;  // past kk the lists are not exact
   int32_t status = kStOk;
   uint32_t token = kInvalidId;
@@ -248,35 +302,57 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
       token = id;
   } else {
     // fg_sampler_select (src/sampler.c:80-122) over the exact top_k, in value
-    // order; the f64 running sums are parallel prefix sums.
-    const uint32_t topk = p.top_k;
+    // order; the f64 running sums are parallel prefix sums.  A whole-row
+    // nucleus (top_k 0) runs the same steps with limit = every finite logit:
+    // its raw sum is the row's mass zz, and the cut must fall inside the
+    // kMaxK best (or the row has no more finite logits than that).
+    const uint32_t topk = nuc ? kMaxK : p.top_k;
     const uint64_t sorted = value_order(lane < topk ? fin : 0ull);
     const uint32_t kept = static_cast<uint32_t>(__popcll(ballot(sorted != 0ull)));
     if (kept == 0u) {
       status = kStFormat;
     } else {
       const uint32_t limit = topk < kept ? topk : kept;
+      const bool whole_row_listed = nuc && kept < kMaxK;
       const bool live = lane < limit;
       const double v = live ? static_cast<double>(key_to_float(comp_key(sorted))) : 0.0;
       const double vmax = __longlong_as_double(static_cast<long long>(
           readlane64(static_cast<uint64_t>(__double_as_longlong(v)), 0)));
       const double e = live ? exp(v - vmax) : 0.0;
       const double ecum = wave_prefix_sum_f64(e);
-      const double sum = __longlong_as_double(static_cast<long long>(
+      double sum = __longlong_as_double(static_cast<long long>(
           readlane64(static_cast<uint64_t>(__double_as_longlong(ecum)), limit - 1u)));
+      // Relative error bound of the f32-term mass (see Mass).
+      double bound = 0.0;
+      if (nuc && !whole_row_listed) {
+        sum = zs.z * exp(zs.m - vmax);
+        bound = 1.2e-7 + 1.8e-7 * (zs.e / zs.z);
+      }
       if (!(sum > 0.0) || !isfinite(sum)) {
         status = kStFormat;
       } else {
         const double cum = wave_prefix_sum_f64(e / sum);
         const uint64_t hit = ballot(live && cum >= static_cast<double>(p.top_p));
-        const uint32_t cutoff = hit ? static_cast<uint32_t>(__builtin_ctzll(hit)) + 1u : limit;
+        uint32_t cutoff = hit ? static_cast<uint32_t>(__builtin_ctzll(hit)) + 1u : limit;
+        // A deeper cut, or a list that ends on zeros (where key order, +0
+        // above -0, and value order, 0 == -0, may keep different entries),
+        // is left to the deep-row kernel.
+        const uint32_t edge_key = comp_key(readlane64(fin, kMaxK - 1u));
+        const bool zero_edge = edge_key == 0x7fffffffu || edge_key == 0x80000000u;
+        // So is a cut that the mass's error bound could move: the positions
+        // either side of the cut must clear top_p by twice the bound.
+        const double gap = lane < cutoff ? fabs(cum - static_cast<double>(p.top_p)) : INFINITY;
+        const bool close = -wave_max_f64(-gap) <= 2.0 * bound;
+        if (nuc && !whole_row_listed && (hit == 0ull || zero_edge || close)) status = kStLimit;
         const double t = static_cast<double>(p.temperature);
         const double vmax_t = vmax / t;
         const double te = lane < cutoff ? exp(v / t - vmax_t) : 0.0;
         const double tcum = wave_prefix_sum_f64(te);
         const double tsum = __longlong_as_double(static_cast<long long>(
             readlane64(static_cast<uint64_t>(__double_as_longlong(tcum)), cutoff - 1u)));
-        if (!(tsum > 0.0) || !isfinite(tsum)) {
+        if (status != kStOk) {
+          // whole-row nucleus cut below the kMaxK best: no token
+        } else if (!(tsum > 0.0) || !isfinite(tsum)) {
           status = kStFormat;
         } else {
           float u = a.uniforms[row];
@@ -310,6 +386,10 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
       a.lp_ids[static_cast<uint64_t>(row) * L + lane] = id;
     }
   }
+  if (nuc && lane == 0) {
+    a.nuc_deep[row] = status == kStLimit ? 1u : 0u;
+    a.nuc_max[row] = key_to_float(comp_key(readlane64(fin, 0)));
+  }
   if (lane == 0) {
     a.tokens[row] = token;
     if (a.token_logits) a.token_logits[row] = token_logit;
@@ -321,13 +401,14 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
 
 // Which parts of the pass a launch needs (the union over its rows).  Each
 // combination is its own instantiation, so a launch carries only its code.
-template <bool kVec_, bool kPen_, bool kGreedy_, bool kTop_, bool kLse_>
+template <bool kVec_, bool kPen_, bool kGreedy_, bool kTop_, bool kLse_, bool kNuc_>
 struct Features {
   static constexpr bool kVec = kVec_;      // 16-byte aligned rows: vector loads
   static constexpr bool kPen = kPen_;      // some row applies penalties
   static constexpr bool kGreedy = kGreedy_;  // some row is greedy
   static constexpr bool kTop = kTop_;      // some row keeps a top list
   static constexpr bool kLse = kLse_;      // log-probs requested
+  static constexpr bool kNuc = kNuc_;      // some row is a whole-row nucleus (top_k 0)
 };
 
 template <bool kVec>
@@ -351,6 +432,9 @@ struct WaveState {
   uint32_t gnf;  // greedy: first non-finite id seen by this lane
   float lm;      // per-lane max of finite s
   float lz;      // per-lane sum exp2((s - lm) * log2e / T)
+  float nm;      // nucleus: per-lane max of finite s
+  double nz;     // nucleus: per-lane sum of f32 terms exp(s - nm)
+  double ne;     // nucleus: per-lane sum exp(s - nm) (nm - s), the error bound
   bool first;
 };
 
@@ -385,7 +469,7 @@ __device__ __forceinline__ uint64_t greedy_lane_comp(const WaveState& st) {
 // at or past q_end are clamped duplicates and are masked out.
 template <class F>
 __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, bool pen,
-                                             bool greedy, bool lse, float log2e_over_t,
+                                             bool greedy, bool lse, bool nuc, float log2e_over_t,
                                              float* prow, const f4* x, const u4* y, uint32_t q0,
                                              uint32_t q_end) {
   const uint32_t lane = lane_id();
@@ -450,6 +534,38 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
         if (ok[j] && is_finite_bits(__float_as_uint(v[j][e])))
           st.lz += exp2f((v[j][e] - st.lm) * log2e_over_t);
   }
+  if (F::kNuc && nuc) {
+    float step_max = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kStepVec; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (ok[j] && is_finite_bits(__float_as_uint(v[j][e]))) step_max = fmaxf(step_max, v[j][e]);
+    if (step_max > st.nm) {
+      if (st.nm == -INFINITY) {
+        st.nz = st.ne = 0.0;
+      } else {
+        const double d = static_cast<double>(step_max) - static_cast<double>(st.nm);
+        const double f = exp(-d);
+        st.ne = f * (st.ne + d * st.nz);
+        st.nz = f * st.nz;
+      }
+      st.nm = step_max;
+    }
+    // f32 terms summed in f64; their error bound sum w * (max - s) in f32.
+    float ef = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kStepVec; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (ok[j] && is_finite_bits(__float_as_uint(v[j][e]))) {
+          const float sd = v[j][e] - st.nm;
+          const float w = exp2f(sd * 1.4426950408889634f);
+          st.nz += static_cast<double>(w);
+          ef = fmaf(w, -sd, ef);
+        }
+    st.ne += static_cast<double>(ef);
+  }
   if (F::kTop && st.t.kk) {
     if (st.first) {
       // The kk-th largest lane maximum: at least kk keys of this step are >=
@@ -485,6 +601,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   __shared__ uint64_t s_greedy[kWaves];
   __shared__ double s_lm[kWaves];
   __shared__ double s_lz[kWaves];
+  __shared__ double s_nm[kWaves];
+  __shared__ double s_nz[kWaves];
+  __shared__ double s_ne[kWaves];
   __shared__ int s_last;
 
   const uint32_t wave = threadIdx.x / kWave;
@@ -495,7 +614,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const bool greedy = p.temperature == 0.0f;
   const uint32_t L = a.logprobs;
   const bool lse = F::kLse && L != 0u;
-  const uint32_t kk = greedy ? L : (p.top_k > L ? p.top_k : L);
+  const bool nuc = F::kNuc && !greedy && p.top_k == 0u;
+  const uint32_t kk = greedy ? L : nuc ? kMaxK : (p.top_k > L ? p.top_k : L);
   const bool pen = (p.flags & kRowPenalties) && a.counts != nullptr;
   const float t_eff = p.temperature > 0.0f ? p.temperature : 1.0f;
   const float log2e_over_t = 1.4426950408889634f / t_eff;
@@ -511,7 +631,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
 
   WaveState st{{0ull, kFiniteComp - 1ull, F::kTop ? s_buf[wave] : nullptr, 0u, F::kTop ? kk : 0u,
                 -3.402823466e38f},
-               -INFINITY, kInvalidId, kInvalidId, -INFINITY, 0.0f, true};
+               -INFINITY, kInvalidId, kInvalidId, -INFINITY, 0.0f, -INFINITY, 0.0, 0.0, true};
   FG_TRACE(a, 0);
 
   if (q_end > q_begin) {
@@ -529,7 +649,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       for (int j = 0; j < kStepVec; j++)
         load_quad<F::kVec>(lrow, crow, F::kPen && pen, min(qn + j * kWave + lane, q_end - 1u),
                            xb[j], yb[j]);
-      process_step<F>(st, p, pen, greedy, lse, log2e_over_t, prow, xa, ya, q0, q_end);
+      process_step<F>(st, p, pen, greedy, lse, nuc, log2e_over_t, prow, xa, ya, q0, q_end);
 #pragma unroll
       for (int j = 0; j < kStepVec; j++) {
         xa[j] = xb[j];
@@ -557,6 +677,14 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
           }
           st.lz += exp2f((v - st.lm) * log2e_over_t);
         }
+        if (F::kNuc && nuc && valid && is_finite_bits(__float_as_uint(v))) {
+          // Exact f64 terms here (error bound contribution 0).
+          Mass ms{static_cast<double>(st.nm), st.nz, st.ne};
+          mass_accumulate(ms, static_cast<double>(v), 1.0, 0.0);
+          st.nm = static_cast<float>(ms.m);
+          st.nz = ms.z;
+          st.ne = ms.e;
+        }
         if (F::kTop && kk) top_stage(st.t, make_comp(valid ? float_key(v) : 0u, i0 + e));
       }
     }
@@ -570,10 +698,13 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint64_t gbest = (F::kGreedy && greedy) ? wave_max_u64(greedy_lane_comp(st)) : 0ull;
   double wm = -INFINITY, wz = 0.0;
   if (lse) wave_lse_combine(static_cast<double>(st.lm), static_cast<double>(st.lz), t_eff, &wm, &wz);
+  Mass wmass{-INFINITY, 0.0, 0.0};
+  if (F::kNuc && nuc) wmass = wave_mass_combine(static_cast<double>(st.nm), st.nz, st.ne);
 
   uint64_t fin = 0ull;
   uint64_t g = 0ull;
   double m = -INFINITY, z = 0.0;
+  Mass zs{-INFINITY, 0.0, 0.0};
   if (a.chunks == 1u) {
     // The whole row is in this workgroup: merge from LDS.
     if (F::kTop) s_top[wave][lane] = mine;
@@ -581,6 +712,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       s_greedy[wave] = gbest;
       s_lm[wave] = wm;
       s_lz[wave] = wz;
+      s_nm[wave] = wmass.m;
+      s_nz[wave] = wmass.z;
+      s_ne[wave] = wmass.e;
     }
     __syncthreads();
     if (wave != 0) return;
@@ -590,12 +724,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     }
     for (int w = 0; w < kWaves; w++) {
       g = s_greedy[w] > g ? s_greedy[w] : g;
-      m = s_lm[w] > m ? s_lm[w] : m;
+      if (lse) lse_accumulate(m, z, s_lm[w], s_lz[w], t_eff);
+      if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
     }
-    if (lse && m != -INFINITY)
-      for (int w = 0; w < kWaves; w++)
-        if (s_lm[w] != -INFINITY) z += s_lz[w] * exp((s_lm[w] - m) / t_eff);
-    finish_row(a, p, row, fin, g, m, z, lrow, crow, pen);
+    finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen);
     return;
   }
 
@@ -607,6 +739,11 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (lse) {
       store_coherent_f64(a.lse + slot * 2, wm);
       store_coherent_f64(a.lse + slot * 2 + 1, wz);
+    }
+    if (F::kNuc && nuc) {
+      store_coherent_f64(a.zsum + slot * 3, wmass.m);
+      store_coherent_f64(a.zsum + slot * 3 + 1, wmass.z);
+      store_coherent_f64(a.zsum + slot * 3 + 2, wmass.e);
     }
   }
   wait_memory();
@@ -657,20 +794,21 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   }
   if (lse) {
     double lm = -INFINITY, lz = 0.0;
-    for (uint32_t i = lane; i < lists; i += kWave) {
-      const double mi = load_coherent_f64(a.lse + (row_slot + i) * 2);
-      const double zi = load_coherent_f64(a.lse + (row_slot + i) * 2 + 1);
-      if (mi == -INFINITY) continue;
-      if (mi > lm) {
-        lz = (lm == -INFINITY) ? 0.0 : lz * exp((lm - mi) / t_eff);
-        lm = mi;
-      }
-      lz += zi * exp((mi - lm) / t_eff);
-    }
+    for (uint32_t i = lane; i < lists; i += kWave)
+      lse_accumulate(lm, lz, load_coherent_f64(a.lse + (row_slot + i) * 2),
+                     load_coherent_f64(a.lse + (row_slot + i) * 2 + 1), t_eff);
     wave_lse_combine(lm, lz, t_eff, &m, &z);
   }
+  if (F::kNuc && nuc) {
+    Mass lm{-INFINITY, 0.0, 0.0};
+    for (uint32_t i = lane; i < lists; i += kWave)
+      mass_accumulate(lm, load_coherent_f64(a.zsum + (row_slot + i) * 3),
+                      load_coherent_f64(a.zsum + (row_slot + i) * 3 + 1),
+                      load_coherent_f64(a.zsum + (row_slot + i) * 3 + 2));
+    zs = wave_mass_combine(lm.m, lm.z, lm.e);
+  }
   FG_TRACE(a, 6);
-  finish_row(a, p, row, fin, g, m, z, lrow, crow, pen);
+  finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen);
   if (lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
   FG_TRACE(a, 7);
 }

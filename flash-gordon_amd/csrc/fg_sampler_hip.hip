@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include "fg_sampler_hip.h"
+#include "fg_nucleus_kernels.hpp"
 #include "fg_sample_kernels.hpp"
 #include "fg_unit_kernels.hpp"
 
@@ -52,18 +53,21 @@ void launch_sample(uint32_t grid, hipStream_t s, const fg::SampleArgs& a) {
 template <int kBits>
 constexpr SampleLaunch vec_launch() {
   return launch_sample<fg::Features<true, (kBits & 1) != 0, (kBits & 2) != 0, (kBits & 4) != 0,
-                                    (kBits & 8) != 0>>;
+                                    (kBits & 8) != 0, (kBits & 16) != 0>>;
 }
 
-// Indexed by pen | greedy << 1 | top << 2 | lse << 3.
-const SampleLaunch kVecLaunch[16] = {
-    vec_launch<0>(),  vec_launch<1>(),  vec_launch<2>(),  vec_launch<3>(),
-    vec_launch<4>(),  vec_launch<5>(),  vec_launch<6>(),  vec_launch<7>(),
-    vec_launch<8>(),  vec_launch<9>(),  vec_launch<10>(), vec_launch<11>(),
-    vec_launch<12>(), vec_launch<13>(), vec_launch<14>(), vec_launch<15>(),
+template <int... kBits>
+struct LaunchTable {
+  static constexpr SampleLaunch table[sizeof...(kBits)] = {vec_launch<kBits>()...};
 };
+
+// Indexed by pen | greedy << 1 | top << 2 | lse << 3 | nucleus << 4.
+const SampleLaunch* const kVecLaunch =
+    LaunchTable<0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21,
+                22, 23, 24, 25, 26, 27, 28, 29, 30, 31>::table;
 // Rows that are not 16-byte aligned: scalar loads, every part compiled in.
-const SampleLaunch kScalarLaunch = launch_sample<fg::Features<false, true, true, true, true>>;
+const SampleLaunch kScalarLaunch =
+    launch_sample<fg::Features<false, true, true, true, true, true>>;
 
 }  // namespace
 
@@ -78,7 +82,10 @@ struct fg_sampler_hip {
   uint64_t* d_cand;         // [slots][kMaxK]
   uint64_t* d_greedy;       // [slots]
   double* d_lse;            // [slots][2]
+  double* d_zsum;           // [slots][3]
   uint32_t* d_row_done;     // [max_rows * kLineWords]
+  uint32_t* d_nuc_deep;     // [max_rows]
+  float* d_nuc_max;         // [max_rows]
   uint32_t target_groups;   // workgroups per launch the chunking aims for
   uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
 };
@@ -204,9 +211,12 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMalloc(&s->d_cand, sizeof(uint64_t) * slots * fg::kMaxK);
   if (e == hipSuccess) e = hipMalloc(&s->d_greedy, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->d_lse, sizeof(double) * slots * 2);
+  if (e == hipSuccess) e = hipMalloc(&s->d_zsum, sizeof(double) * slots * 3);
   const size_t done_bytes = sizeof(uint32_t) * fg::kLineWords * max_rows;
   if (e == hipSuccess) e = hipMalloc(&s->d_row_done, done_bytes);
   if (e == hipSuccess) e = hipMemset(s->d_row_done, 0, done_bytes);
+  if (e == hipSuccess) e = hipMalloc(&s->d_nuc_deep, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&s->d_nuc_max, sizeof(float) * max_rows);
   if (e == hipSuccess) e = hipMemset(s->d_params, 0, sizeof(RowParams) * max_rows);
 #ifdef FG_SAMPLE_TRACE
   if (e == hipSuccess) e = hipMalloc(&s->trace, sizeof(uint64_t) * 8u * (s->target_groups + max_rows));
@@ -227,7 +237,10 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   (void)hipFree(s->d_cand);
   (void)hipFree(s->d_greedy);
   (void)hipFree(s->d_lse);
+  (void)hipFree(s->d_zsum);
   (void)hipFree(s->d_row_done);
+  (void)hipFree(s->d_nuc_deep);
+  (void)hipFree(s->d_nuc_max);
   (void)hipFree(s->trace);
   free(s->h_params);
   free(s);
@@ -272,12 +285,6 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
       (b->counts && b->counts_stride < s->vocab) || b->logprobs > fg::kMaxK ||
       (b->logprobs && (!b->logprob_values || !b->logprob_ids)))
     return arg_fail(err, "invalid sampled output arguments");
-  for (uint32_t r = 0; r < b->rows; r++) {
-    if (s->h_params[r].temperature > 0.0f && s->h_params[r].top_k == 0u) {
-      fg_error_set(err, FG_ERR_UNAVAILABLE, "whole-vocabulary nucleus is not available yet");
-      return FG_ERR_UNAVAILABLE;
-    }
-  }
   const uint32_t vocab = s->vocab;
   // Chunking: aim for target_groups workgroups, at most kMaxChunks per row,
   // each wave slice a multiple of 4 elements.
@@ -315,23 +322,30 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
   a.cand = s->d_cand;
   a.greedy = s->d_greedy;
   a.lse = s->d_lse;
+  a.zsum = s->d_zsum;
   a.row_done = s->d_row_done;
+  a.nuc_deep = s->d_nuc_deep;
+  a.nuc_max = s->d_nuc_max;
   a.trace = s->trace;
 
   const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
                    (!b->counts || (aligned16(b->counts) && (b->counts_stride % 4u) == 0u));
-  bool any_pen = false, any_greedy = false, any_top = b->logprobs != 0u;
+  bool any_pen = false, any_greedy = false, any_top = b->logprobs != 0u, any_nuc = false;
   for (uint32_t r = 0; r < b->rows; r++) {
     const RowParams& rp = s->h_params[r];
     any_pen |= (rp.flags & fg::kRowPenalties) != 0u;
     any_greedy |= rp.temperature == 0.0f;
     any_top |= rp.temperature > 0.0f;
+    any_nuc |= rp.temperature > 0.0f && rp.top_k == 0u;
   }
   any_pen = any_pen && b->counts != nullptr;
   const int bits = (any_pen ? 1 : 0) | (any_greedy ? 2 : 0) | (any_top ? 4 : 0) |
-                   (b->logprobs ? 8 : 0);
+                   (b->logprobs ? 8 : 0) | (any_nuc ? 16 : 0);
   const uint32_t grid = b->rows * chunks;
   (vec ? kVecLaunch[bits] : kScalarLaunch)(grid, as_stream(stream), a);
+  // Whole-row nucleus rows whose cut lies past the kMaxK best are finished
+  // by a second kernel; the others return at once.
+  if (any_nuc) fg::nucleus_rows_kernel<<<b->rows, fg::kNucBlock, 0, as_stream(stream)>>>(a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "sampler launch");
 }

@@ -92,8 +92,12 @@ fg_status fg_hip_history_build(uint32_t *counts, uint64_t counts_stride, uint32_
 typedef struct fg_sampler_hip fg_sampler_hip;
 
 /* Extension flag for fg_sampler_hip_set_configs: accept top_k == 0, meaning
- * "no top-k" (nucleus over the whole vocabulary).  The reference rejects
- * top_k == 0 (src/sampler.c:27); without this flag so does this library. */
+ * "no top-k": fg_sampler_select (src/sampler.c:80-122) over every finite
+ * logit of the row (nucleus over the whole vocabulary).  The reference
+ * rejects top_k == 0 (src/sampler.c:27); without this flag so does this
+ * library.  Such rows are finished in the fused pass when the cut falls
+ * inside the row's 64 best logits, otherwise by a second kernel launched on
+ * the same stream (histogram descent over the whole row). */
 #define FG_SAMPLER_HIP_ALLOW_FULL_VOCAB 1u
 
 /* Creates a sampler for rows of `vocab` logits and up to `max_rows` rows per
@@ -126,14 +130,17 @@ typedef struct fg_sampler_hip_batch {
     uint32_t *logprob_ids;      /* out: rows x logprobs */
 } fg_sampler_hip_batch;
 
-/* Samples one token per row in one launch.  Per row, with the row's config:
+/* Samples one token per row in one launch (two when a row has top_k == 0).
+ * Per row, with the row's config:
  *   penalties (when fg_sampler_penalties_active and counts != NULL),
  *   T == 0: argmax with the reference's greedy order; a non-finite winner sets
  *           row_status FG_ERR_MISMATCH (no penalties, src/output.c:593) or
  *           FG_ERR_FORMAT (penalties, src/output.c:736-740);
  *   T  > 0: exact top_k by float key, then fg_sampler_select's arithmetic on
  *           those candidates with the row's uniform (src/sampler.c:80-122);
- *           top_k == 0 (extension) runs the same rule over the whole row.
+ *           top_k == 0 (extension) runs the same rule over the whole row
+ *           (FG_ERR_LIMIT only if that search finds no element, which a
+ *           row with a finite logit does not produce).
  * Log-probs: the first `logprobs` of the row's max(top_k, logprobs) best
  * candidates ordered by (value desc, id asc), lp = s/T - logsumexp_j(s_j/T)
  * over the finite penalised logits of the row (T == 0 uses T = 1).

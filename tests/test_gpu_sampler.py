@@ -16,6 +16,11 @@ pytestmark = pytest.mark.gpu
 
 BOUNDARY = 1e-6
 LP_TOL = 1e-5
+# Whole-row nucleus masses are summed with an f64 exp of a few ulp: tokens
+# must match the oracle except where its sums come within 1e-11 of a
+# boundary (1e-6, would excuse most deep cuts, whose
+# steps are ~1e-5 of the mass each).
+NUC_BOUNDARY = 1e-11
 
 
 def to_dev(a, dev):
@@ -56,12 +61,12 @@ def run_hip(w, dev, logprobs=None, penalised=False, flags=0, sampler=None, count
     return out
 
 
-def check(w, got, ref, name):
+def check(w, got, ref, name, boundary=BOUNDARY):
     st_ok = np.array_equal(got["status"], ref["status"])
     assert st_ok, f"{name}: status {got['status']} vs {ref['status']}"
     ok = ref["status"] == 0
     same = got["token"] == ref["token"]
-    near = ref["margin"] < BOUNDARY
+    near = ref["margin"] < boundary
     bad = ok & ~same & ~near
     assert not bad.any(), (
         f"{name}: rows {np.nonzero(bad)[0][:10]} token {got['token'][bad][:10]} "
@@ -203,6 +208,9 @@ def test_argument_errors(dev):
         s.set_configs([fg_hip.make_config(min_p=0.1)])
     with pytest.raises(fg_hip.FgStatusError):
         s.set_configs([fg_hip.make_config(top_k=0)])
+    s.set_configs([fg_hip.make_config(top_k=0)], flags=fg_hip.ALLOW_FULL_VOCAB)
+    with pytest.raises(fg_hip.FgStatusError):
+        s.set_configs([fg_hip.make_config()], flags=4)
     s.set_configs([fg_hip.make_config()] * 4)
     x = torch.zeros((4, 100), device=dev)
     u = torch.zeros(4, device=dev)
@@ -230,3 +238,92 @@ def test_history_increment(dev):
     c = counts.cpu().numpy().view(np.uint32)
     assert c[0, 5] == 1 and c[1, 6] == 0 and c[2, 7] == 0 and c[3, 9] == 0xFFFFFFFF
     assert c.sum(dtype=np.uint64) == 1 + 0xFFFFFFFF
+
+
+def test_config3_whole_row_nucleus(dev):
+    w = W.config3(rows=64)
+    ref = W.oracle_run(w)
+    assert (ref["cutoff"] <= 64).all()
+    check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), ref, "config3", NUC_BOUNDARY)
+
+
+def test_nucleus_cut_depths(dev):
+    """N(0, s^2) rows at T 1: s = 12 and 8 cut inside the 64 best (fused
+    pass), s = 1 thousands deep (deep-row kernel); rows with 100, 40 and 30
+    finite logits."""
+    import oracle_ffi as O
+    vocab = 151_936
+    logits = np.concatenate([O.gen_logits(4, vocab, 0, 12.0, seed=7, config_id=31),
+                             O.gen_logits(4, vocab, 0, 8.0, seed=7, config_id=32),
+                             O.gen_logits(4, vocab, 0, 1.0, seed=7, config_id=33)])
+    rows = logits.shape[0]
+    logits[3, 100:] = np.nan
+    logits[7, 40:] = -np.inf
+    logits[11, 30:] = np.nan
+    configs = [W.cfg(1.0, p, 0, presence=0.3) for p in (0.5, 0.9, 0.95, 0.99)] * 3
+    counts = np.zeros((rows, vocab), dtype=np.uint32)
+    counts[:, ::1000] = 2
+    w = dict(logits=logits, counts=counts, configs=configs,
+             uniforms=np.linspace(0.02, 0.98, rows).astype(np.float32), logprobs=0)
+    ref = W.oracle_run(w)
+    assert (ref["cutoff"] <= 64).sum() >= 6 and (ref["cutoff"] > 1000).sum() >= 2
+    check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), ref, "nucleus depths", NUC_BOUNDARY)
+
+
+def test_nucleus_deep_rows(dev):
+    """Deep cuts: flat rows, whole-row ties (cut and draw inside one value),
+    +0 / -0 mixes, top_p 1 and 0.9999 (cut in the far tail), tempered draws,
+    penalties, and a uniform at each end."""
+    rng = np.random.default_rng(11)
+    vocab = 151_936
+    rows = 12
+    logits = rng.normal(0, 1, (rows, vocab)).astype(np.float32)
+    logits[1, :] = 0.5                               # all tied
+    logits[2, :] = 0.0
+    logits[2, ::2] = -0.0                            # zeros of both signs
+    logits[3, :] = np.round(rng.normal(0, 1, vocab) * 4) / 4   # many ties
+    logits[4, :] = rng.normal(0, 0.01, vocab)        # nearly flat
+    logits[5, :] = rng.normal(0, 6, vocab)           # wide
+    logits[6, : vocab // 2] = np.nan
+    logits[7, :] = np.float32(-1e30)
+    logits[7, 5::7] = np.float32(-1e30) + 1e24
+    configs = [W.cfg(1.0, 0.9, 0), W.cfg(1.0, 0.37, 0), W.cfg(0.8, 0.5, 0, presence=0.0),
+               W.cfg(1.5, 0.95, 0), W.cfg(0.2, 0.9, 0), W.cfg(2.0, 0.999, 0),
+               W.cfg(1.0, 0.7, 0, presence=1.0, frequency=0.5), W.cfg(1.0, 0.6, 0),
+               W.cfg(1.0, 1.0, 0), W.cfg(0.7, 0.9999, 0), W.cfg(3.0, 0.8, 0, repetition=1.3),
+               W.cfg(1.0, 0.9, 0, presence=-0.5)]
+    counts = np.zeros((rows, vocab), dtype=np.uint32)
+    hot = rng.integers(0, vocab, (rows, 5000))
+    np.add.at(counts, (np.repeat(np.arange(rows), 5000), hot.ravel()), 1)
+    u = rng.random(rows).astype(np.float32)
+    u[0], u[8] = 0.0, np.float32(0.99999994)
+    w = dict(logits=logits, counts=counts, configs=configs, uniforms=u, logprobs=3)
+    ref = W.oracle_run(w)
+    assert (ref["cutoff"] > 64).sum() >= 9
+    check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), ref, "deep nucleus", NUC_BOUNDARY)
+
+
+@pytest.mark.parametrize("vocab", [65, 100, 4097, 10_000])
+def test_nucleus_small_vocab(dev, vocab):
+    rng = np.random.default_rng(vocab)
+    rows = 6
+    logits = rng.normal(0, 0.5, (rows, vocab)).astype(np.float32)
+    logits[1, :] = 1.0
+    configs = [W.cfg(1.0, p, 0) for p in (0.3, 0.6, 0.9, 0.99, 1.0, 0.5)]
+    w = dict(logits=logits, counts=np.zeros((rows, vocab), np.uint32), configs=configs,
+             uniforms=rng.random(rows).astype(np.float32), logprobs=0)
+    check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), W.oracle_run(w), f"nucleus {vocab}",
+          NUC_BOUNDARY)
+
+
+def test_nucleus_mixed_with_top_k_rows_and_logprobs(dev):
+    w = W.config3(rows=16, vocab=50_000)
+    for r in range(0, 16, 4):
+        w["configs"][r] = W.cfg(0.7, 0.8, 20, presence=1.5, repetition=1.05)
+    w["configs"][1] = W.cfg(0.0, 1.0, 1)
+    w["configs"][2] = W.cfg(1.0, 0.9, 0)
+    w["logits"][2] = np.random.default_rng(3).normal(0, 1, 50_000).astype(np.float32)
+    w["logprobs"] = 5
+    ref = W.oracle_run(w)
+    assert ref["cutoff"][2] > 64
+    check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), ref, "nucleus mixed", NUC_BOUNDARY)
