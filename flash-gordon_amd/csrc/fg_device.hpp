@@ -179,10 +179,12 @@ __device__ __forceinline__ float penalise(float s, uint32_t c, float pres, float
 // half-row mirror (^7) followed by the quad mirror (^3); 8: row rotate by 8;
 // 16, 32: v_permlane16/32_swap, which hand every lane both members of its pair.
 
+// Every control used here reads a valid lane for every lane, so the DPP
+// "old" operand is never selected and needs no initialising move.
 template <int kCtrl>
 __device__ __forceinline__ uint32_t dpp(uint32_t v) {
   return static_cast<uint32_t>(
-      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xf, 0xf, false));
+      __builtin_amdgcn_mov_dpp(static_cast<int>(v), kCtrl, 0xf, 0xf, false));
 }
 
 template <int J>
@@ -243,11 +245,12 @@ __device__ __forceinline__ T bitonic_step(T v) {
   const bool desc = (K == kWave) || ((lane & K) == 0);
   const bool lower = (lane & J) == 0;
   if constexpr (sizeof(T) == 8) {
-    // Composites compare as f64 (see above): one max and one min.
-    const double a = __longlong_as_double(static_cast<long long>(v));
-    const double b = __longlong_as_double(static_cast<long long>(lane_xor64<J>(v)));
-    const double r = (lower == desc) ? fmax(a, b) : fmin(a, b);
-    return static_cast<T>(__double_as_longlong(r));
+    // One 64-bit compare and two selects; the lane pattern (lower == desc)
+    // folds into the compare's mask.  (An f64 max/min pair would carry two
+    // NaN-quieting canonicalisations per step.)
+    const T o = lane_xor64<J>(v);
+    const bool gt = o > v;
+    return (gt == (lower == desc)) ? o : v;
   } else {
     const T o = lane_xor<J>(v);
     const T hi = o > v ? o : v;

@@ -96,9 +96,18 @@ struct SampleArgs {
       (a).trace[static_cast<uint64_t>(blockIdx.x) * 8u + (slot)] =                 \
           __builtin_amdgcn_s_memrealtime();                                        \
   } while (0)
+// Event counters of FG_SAMPLE_TRACE builds: trace[8 * groups + i].
+__device__ uint64_t* g_trace_counters;
+#define FG_COUNT(i, v)                                                             \
+  do {                                                                             \
+    if (g_trace_counters && lane_id() == 0) atomicAdd(&g_trace_counters[i], (v));  \
+  } while (0)
 #else
 #define FG_TRACE(a, slot) \
   do {                    \
+  } while (0)
+#define FG_COUNT(i, v) \
+  do {                 \
   } while (0)
 #endif
 
@@ -135,6 +144,8 @@ __device__ __forceinline__ void wait_memory() {
 // the list's kk-th entry after each merge: nothing at or below it can enter
 // the top-kk.
 
+constexpr uint64_t kRawTag = 1ull << 63;  // a staged raw entry; composites stay below 2^63
+
 struct TopList {
   uint64_t top;    // lane i: i-th best composite
   uint64_t R;      // filter: a candidate must be > R (wave-uniform)
@@ -142,6 +153,9 @@ struct TopList {
   uint32_t n;      // staged entries (wave-uniform)
   uint32_t kk;     // entries of the list that matter (1..64)
   float fM;        // float form of R for elements later in the stream
+  uint32_t* wg_key;  // LDS, shared by the workgroup's waves: the largest key K
+                     // such that some wave holds kk composites with key >= K
+  uint32_t shared;   // largest key this wave has published
 };
 
 // Raises R.  For an element later in the stream than every list member, a
@@ -155,9 +169,27 @@ __device__ __forceinline__ void top_raise(TopList& t, uint64_t R) {
   t.fM = m < 0x00800000u ? -3.402823466e38f : key_to_float(m);
 }
 
+// The workgroup's waves share their bounds: kk composites with key >= K in
+// one wave mean that no element with a lower key, in any wave of the row, is
+// in the row's top-kk.  Ties on K are kept (their ids may rank either way).
+// (Sharing across the row's workgroups through a global atomic measured
+// slower: a slice is a few steps long, so the bound arrives after most of its
+// staging is done.)
+__device__ __forceinline__ void top_share(TopList& t, uint32_t key) {
+  if (key <= t.shared) return;
+  t.shared = key;
+  if (lane_id() == 0) atomicMax(t.wg_key, key);
+}
+__device__ __forceinline__ void top_adopt(TopList& t) {
+  const uint32_t K = __hip_atomic_load(t.wg_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (K) top_raise(t, key_floor(K));
+}
+
 __device__ __forceinline__ void top_merge_sorted(TopList& t, uint64_t sorted_desc) {
   t.top = wave_merge_desc(t.top, sorted_desc);
-  top_raise(t, readlane64(t.top, t.kk - 1u));
+  const uint64_t kth = readlane64(t.top, t.kk - 1u);
+  top_raise(t, kth);
+  top_share(t, comp_key(kth));
 }
 
 // Moves staged entries into the list: whole groups of 64, or everything when
@@ -170,8 +202,12 @@ __device__ __forceinline__ void top_drain(TopList& t, bool all) {
     uint64_t x = lane < take ? t.buf[at + lane] : 0ull;
     wave_lds_sync();
     t.n = at;
+    if (x & kRawTag)
+      x = make_comp(float_key(__uint_as_float(static_cast<uint32_t>(x))),
+                    static_cast<uint32_t>(x >> 32) & 0x7fffffffu);
     if (x <= t.R) x = 0ull;  // beaten by a list that grew after it was staged
     if (ballot(x != 0ull) == 0ull) continue;
+    FG_COUNT(all ? 3 : 0, 1ull);
     top_merge_sorted(t, wave_sort_desc(x));
   }
 }
@@ -186,12 +222,18 @@ __device__ __forceinline__ void top_stage(TopList& t, uint64_t comp) {
 }
 
 // Stream form: stages value v (element `id`, later in the stream than every
-// list member) when it passes the float filter.
+// list member) when it passes the float filter.  The entry is staged raw
+// (id << 32 | float bits, marked by kRawTag) and becomes a composite when it
+// is drained: the per-element cost stays a compare, a count and one store.
+// +Inf passes the filter and is dropped at the drain (its key is 0).
 __device__ __forceinline__ void top_stage_stream(TopList& t, bool valid, float v, uint32_t id) {
-  const bool pass = valid && v >= t.fM && v < INFINITY;
+  const bool pass = valid && v >= t.fM;
   const uint64_t m = ballot(pass);
   if (m == 0ull) return;
-  if (pass) t.buf[t.n + lanes_below(m)] = make_comp(float_key(v), id);
+  FG_COUNT(1, static_cast<unsigned long long>(__popcll(m)));
+  if (pass)
+    t.buf[t.n + lanes_below(m)] =
+        kRawTag | (static_cast<uint64_t>(id) << 32) | __float_as_uint(v);
   t.n += static_cast<uint32_t>(__popcll(m));
 }
 
@@ -425,6 +467,23 @@ __device__ __forceinline__ void load_quad(const float* lrow, const uint32_t* cro
   }
 }
 
+// Vector path: raw buffer loads over the wave's slice.  The descriptor's
+// range ends at the slice's last quad, so a load past it returns zeros
+// without a memory request: the double-buffered loop loads the "next" step
+// unconditionally, and the step after the slice costs nothing to wait for.
+constexpr int32_t kBufferWord3 = 0x00020000;  // 32-bit data format, raw access
+constexpr int32_t kLoadNT = 2;                // non-temporal (streamed once)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
+                                           kBufferWord3);
+}
+__device__ __forceinline__ void load_quad_buf(__amdgpu_buffer_rsrc_t rl, __amdgpu_buffer_rsrc_t rc,
+                                              bool pen, uint32_t qrel, f4& x, u4& y) {
+  x = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rl, qrel * 16u, 0, kLoadNT));
+  y = pen ? __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rc, qrel * 16u, 0, kLoadNT))
+          : u4{0u, 0u, 0u, 0u};
+}
+
 struct WaveState {
   TopList t;
   float gv;      // greedy: best value seen by this lane (stream order breaks ties)
@@ -578,17 +637,38 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
           const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
           lane_max_key = key > lane_max_key ? key : lane_max_key;
         }
-      const uint32_t T = readlane32(wave_sort_desc_u32(lane_max_key), st.t.kk - 1u);
+      // Largest T (to 2^12 key units) with at least kk lane maxima >= T: a
+      // ballot radix search, cheaper than sorting the 64 maxima.
+      uint32_t T = 0u;
+#pragma unroll
+      for (int b = 31; b >= 12; b--) {
+        const uint32_t c = T | (1u << b);
+        if (static_cast<uint32_t>(__popcll(ballot(lane_max_key >= c))) >= st.t.kk) T = c;
+      }
       if (T) top_raise(st.t, key_floor(T));
+      top_share(st.t, T);
       st.first = false;
+    } else {
+      top_adopt(st.t);
     }
+    // Most steps hold no candidate once the filter has risen: one ballot on
+    // the lane maxima skips the per-element staging.
+    float lane_max = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++) {
-      const uint32_t q = q0 + j * kWave + lane;
+    for (int j = 0; j < kStepVec; j++)
 #pragma unroll
-      for (int e = 0; e < 4; e++) top_stage_stream(st.t, ok[j], v[j][e], q * 4u + e);
+      for (int e = 0; e < 4; e++)
+        if (ok[j] && v[j][e] < INFINITY) lane_max = fmaxf(lane_max, v[j][e]);
+    if (ballot(lane_max >= st.t.fM) != 0ull) {
+      FG_COUNT(2, 1ull);
+#pragma unroll
+      for (int j = 0; j < kStepVec; j++) {
+        const uint32_t q = q0 + j * kWave + lane;
+#pragma unroll
+        for (int e = 0; e < 4; e++) top_stage_stream(st.t, ok[j], v[j][e], q * 4u + e);
+      }
+      top_drain(st.t, false);
     }
-    top_drain(st.t, false);
   }
 }
 
@@ -605,6 +685,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   __shared__ double s_nz[kWaves];
   __shared__ double s_ne[kWaves];
   __shared__ int s_last;
+  __shared__ uint32_t s_wg_key;
 
   const uint32_t wave = threadIdx.x / kWave;
   const uint32_t lane = lane_id();
@@ -629,26 +710,37 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint32_t q_begin = wbegin / 4u;
   const uint32_t q_end = (wbegin + ((wend - wbegin) & ~3u)) / 4u;
 
+  if (F::kTop) {
+    if (threadIdx.x == 0) s_wg_key = 0u;
+    __syncthreads();
+  }
   WaveState st{{0ull, kFiniteComp - 1ull, F::kTop ? s_buf[wave] : nullptr, 0u, F::kTop ? kk : 0u,
-                -3.402823466e38f},
+                -3.402823466e38f, &s_wg_key, 0u},
                -INFINITY, kInvalidId, kInvalidId, -INFINITY, 0.0f, -INFINITY, 0.0, 0.0, true};
   FG_TRACE(a, 0);
 
   if (q_end > q_begin) {
-    // Double-buffered: step s+1 is loaded (addresses clamped into the slice)
-    // before step s is processed, so loads stay in flight.
+    // Double-buffered: step s+1 is loaded before step s is processed, so
+    // loads stay in flight.  (Loading further ahead measured slower.)
     f4 xa[kStepVec], xb[kStepVec];
     u4 ya[kStepVec], yb[kStepVec];
+    const bool cnt = F::kPen && pen;
+    const uint32_t slice_bytes = (q_end - q_begin) * 16u;
+    const __amdgpu_buffer_rsrc_t rl = slice_rsrc(lrow + 4u * q_begin, slice_bytes);
+    const __amdgpu_buffer_rsrc_t rc =
+        slice_rsrc(cnt ? static_cast<const void*>(crow + 4u * q_begin) : lrow, slice_bytes);
+    auto load = [&](f4 (&x)[kStepVec], u4 (&y)[kStepVec], uint32_t qs) {
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++)
-      load_quad<F::kVec>(lrow, crow, F::kPen && pen, min(q_begin + j * kWave + lane, q_end - 1u),
-                         xa[j], ya[j]);
+      for (int j = 0; j < kStepVec; j++) {
+        if constexpr (F::kVec)
+          load_quad_buf(rl, rc, cnt, qs - q_begin + j * kWave + lane, x[j], y[j]);
+        else
+          load_quad<false>(lrow, crow, cnt, min(qs + j * kWave + lane, q_end - 1u), x[j], y[j]);
+      }
+    };
+    load(xa, ya, q_begin);
     for (uint32_t q0 = q_begin; q0 < q_end; q0 += kStepQuads) {
-      const uint32_t qn = q0 + kStepQuads;
-#pragma unroll
-      for (int j = 0; j < kStepVec; j++)
-        load_quad<F::kVec>(lrow, crow, F::kPen && pen, min(qn + j * kWave + lane, q_end - 1u),
-                           xb[j], yb[j]);
+      load(xb, yb, q0 + kStepQuads);
       process_step<F>(st, p, pen, greedy, lse, nuc, log2e_over_t, prow, xa, ya, q0, q_end);
 #pragma unroll
       for (int j = 0; j < kStepVec; j++) {

@@ -88,6 +88,7 @@ struct fg_sampler_hip {
   float* d_nuc_max;         // [max_rows]
   uint32_t target_groups;   // workgroups per launch the chunking aims for
   uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
+  uint64_t* counters;       // event counters, FG_SAMPLE_TRACE builds only
 };
 
 extern "C" {
@@ -221,6 +222,10 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
 #ifdef FG_SAMPLE_TRACE
   if (e == hipSuccess) e = hipMalloc(&s->trace, sizeof(uint64_t) * 8u * (s->target_groups + max_rows));
   if (e == hipSuccess) e = hipMemset(s->trace, 0, sizeof(uint64_t) * 8u * (s->target_groups + max_rows));
+  if (e == hipSuccess) e = hipMalloc(&s->counters, sizeof(uint64_t) * 16u);
+  if (e == hipSuccess) e = hipMemset(s->counters, 0, sizeof(uint64_t) * 16u);
+  if (e == hipSuccess)
+    e = hipMemcpyToSymbol(HIP_SYMBOL(fg::g_trace_counters), &s->counters, sizeof(uint64_t*));
 #endif
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
@@ -328,7 +333,9 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
   a.nuc_max = s->d_nuc_max;
   a.trace = s->trace;
 
+  // The vector path addresses a slice with 32-bit byte offsets.
   const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
+                   wave_elems < (1u << 28) &&
                    (!b->counts || (aligned16(b->counts) && (b->counts_stride % 4u) == 0u));
   bool any_pen = false, any_greedy = false, any_top = b->logprobs != 0u, any_nuc = false;
   for (uint32_t r = 0; r < b->rows; r++) {
@@ -368,6 +375,12 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
 // Copies the last launch's phase timestamps ([workgroup][8]) to the host.
 fg_status fg_sampler_hip_trace_copy(fg_sampler_hip* s, uint64_t* host, uint64_t count) {
   const hipError_t e = hipMemcpy(host, s->trace, sizeof(uint64_t) * count, hipMemcpyDeviceToHost);
+  return e == hipSuccess ? FG_OK : FG_ERR_UNAVAILABLE;
+}
+// Copies the event counters (16 u64) to the host and clears them.
+fg_status fg_sampler_hip_trace_counters(fg_sampler_hip* s, uint64_t* host) {
+  hipError_t e = hipMemcpy(host, s->counters, sizeof(uint64_t) * 16u, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemset(s->counters, 0, sizeof(uint64_t) * 16u);
   return e == hipSuccess ? FG_OK : FG_ERR_UNAVAILABLE;
 }
 #endif
