@@ -128,7 +128,7 @@ __device__ __forceinline__ void for_each_element(const RowView& r, Fn&& f) {
 // returns the totals.  All threads must call it.
 __device__ inline void block_scan2(NucLds& s, double a, double b, double* ea, double* eb,
                                    double* ta, double* tb) {
-  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform
   const uint32_t lane = lane_id();
   const double ia = wave_prefix_sum_f64(a);
   const double ib = wave_prefix_sum_f64(b);

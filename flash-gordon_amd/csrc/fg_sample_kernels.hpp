@@ -192,23 +192,75 @@ __device__ __forceinline__ void top_merge_sorted(TopList& t, uint64_t sorted_des
   top_share(t, comp_key(kth));
 }
 
+__device__ __forceinline__ uint64_t staged_comp(uint64_t x) {
+  return (x & kRawTag) ? make_comp(float_key(__uint_as_float(static_cast<uint32_t>(x))),
+                                   static_cast<uint32_t>(x >> 32) & 0x7fffffffu)
+                       : x;
+}
+
+// Raises the filter from the staged entries alone and drops those it beats,
+// without sorting: the kk-th largest of the lanes' maximum staged keys (a
+// ballot radix search, to 2^12 key units) has at least kk staged entries at
+// or above it.  Cheaper than sorting 64 entries into the list, it usually
+// leaves fewer than 64 staged.
+__device__ __forceinline__ void top_select(TopList& t) {
+  const uint32_t lane = lane_id();
+  uint32_t kmax = 0u;
+  for (uint32_t i = lane; i < t.n; i += kWave) {
+    const uint32_t k = comp_key(staged_comp(t.buf[i]));
+    kmax = k > kmax ? k : kmax;
+  }
+  uint32_t T = 0u;
+#pragma unroll
+  for (int b = 31; b >= 12; b--) {
+    const uint32_t c = T | (1u << b);
+    if (static_cast<uint32_t>(__popcll(ballot(kmax >= c))) >= t.kk) T = c;
+  }
+  if (T) {
+    top_raise(t, key_floor(T));
+    top_share(t, T);
+  }
+  // Compact in place: a chunk is read before anything is written over it.
+  uint32_t w = 0u;
+  for (uint32_t c = 0; c < t.n; c += kWave) {
+    uint64_t x = c + lane < t.n ? staged_comp(t.buf[c + lane]) : 0ull;
+    wave_lds_sync();
+    const bool keep = x > t.R;
+    const uint64_t m = ballot(keep);
+    if (keep) t.buf[w + lanes_below(m)] = x;
+    w += static_cast<uint32_t>(__popcll(m));
+    wave_lds_sync();
+  }
+  t.n = w;
+}
+
 // Moves staged entries into the list: whole groups of 64, or everything when
-// `all` is set.
+// `all` is set.  While streaming (kk <= 32), a full stage is first thinned by
+// top_select; only what still fills 64 entries is sorted in.  (For larger kk
+// the lanes' maxima rarely raise the filter.)  An empty list takes a sorted
+// group as it is.
 __device__ __forceinline__ void top_drain(TopList& t, bool all) {
   const uint32_t lane = lane_id();
+  if (!all && t.kk <= 32u && t.n >= static_cast<uint32_t>(kWave)) top_select(t);
   while (t.n >= static_cast<uint32_t>(kWave) || (all && t.n > 0u)) {
     const uint32_t take = t.n < static_cast<uint32_t>(kWave) ? t.n : static_cast<uint32_t>(kWave);
     const uint32_t at = t.n - take;
     uint64_t x = lane < take ? t.buf[at + lane] : 0ull;
     wave_lds_sync();
     t.n = at;
-    if (x & kRawTag)
-      x = make_comp(float_key(__uint_as_float(static_cast<uint32_t>(x))),
-                    static_cast<uint32_t>(x >> 32) & 0x7fffffffu);
+    x = staged_comp(x);
     if (x <= t.R) x = 0ull;  // beaten by a list that grew after it was staged
     if (ballot(x != 0ull) == 0ull) continue;
     FG_COUNT(all ? 3 : 0, 1ull);
-    top_merge_sorted(t, wave_sort_desc(x));
+    const uint64_t sorted = wave_sort_desc(x);
+    if (ballot(t.top != 0ull) == 0ull) {
+      t.top = sorted;
+      const uint64_t kth = readlane64(t.top, t.kk - 1u);
+      top_raise(t, kth);
+      top_share(t, comp_key(kth));
+    } else {
+      top_merge_sorted(t, sorted);
+    }
   }
 }
 
@@ -687,7 +739,11 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   __shared__ int s_last;
   __shared__ uint32_t s_wg_key;
 
-  const uint32_t wave = threadIdx.x / kWave;
+  // readfirstlane: the wave index is uniform across the wave, so the slice
+  // bounds, buffer descriptors and loop control stay scalar (the compiler
+  // treats threadIdx.x / 64 as divergent, which wraps every buffer load in a
+  // waterfall loop).
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t lane = lane_id();
   const uint32_t row = blockIdx.x / a.chunks;
   const uint32_t chunk = blockIdx.x - row * a.chunks;
@@ -720,8 +776,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   FG_TRACE(a, 0);
 
   if (q_end > q_begin) {
-    // Double-buffered: step s+1 is loaded before step s is processed, so
-    // loads stay in flight.  (Loading further ahead measured slower.)
+    // Double-buffered, the two buffers taking turns (no register copies,
+    // which would wait for the loads on the back edge): step s+1 is loaded
+    // before step s is processed.  (Loading further ahead measured slower.)
     f4 xa[kStepVec], xb[kStepVec];
     u4 ya[kStepVec], yb[kStepVec];
     const bool cnt = F::kPen && pen;
@@ -739,14 +796,13 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       }
     };
     load(xa, ya, q_begin);
-    for (uint32_t q0 = q_begin; q0 < q_end; q0 += kStepQuads) {
+    for (uint32_t q0 = q_begin;;) {
       load(xb, yb, q0 + kStepQuads);
       process_step<F>(st, p, pen, greedy, lse, nuc, log2e_over_t, prow, xa, ya, q0, q_end);
-#pragma unroll
-      for (int j = 0; j < kStepVec; j++) {
-        xa[j] = xb[j];
-        ya[j] = yb[j];
-      }
+      if ((q0 += kStepQuads) >= q_end) break;
+      load(xa, ya, q0 + kStepQuads);
+      process_step<F>(st, p, pen, greedy, lse, nuc, log2e_over_t, prow, xb, yb, q0, q_end);
+      if ((q0 += kStepQuads) >= q_end) break;
     }
   }
   {

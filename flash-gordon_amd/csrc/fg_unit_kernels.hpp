@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void argmax_reduce_kernel(float* out_scores, u
     const float ov = __shfl_xor(best_v, d);
     if (o > best) { best = o; best_v = ov; }
   }
-  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform
   if (lane_id() == 0) { s_comp[wave] = best; s_val[wave] = best_v; }
   __syncthreads();
   if (threadIdx.x == 0) {
