@@ -1,17 +1,24 @@
 """Benchmark of the batched sampler on one MI355X.
 
-Workload: BASELINE.json config 2 (the north star) -- 64 rows x 151,936 f32
-logits N(0, 3^2) with 5 ids/row boosted by +8, per-row history counts from
-1,024 Zipf(1.1) ids, presence 1.5 + repetition 1.05, T 0.7, top-k 20,
-top-p 0.8, one uniform per row.  A step is one fg_sampler_hip_sample launch
-over one batch.  Inputs are generated on the device with torch (synthetic) and
-rotated over >= 4 GB of distinct batches so the 256 MB Infinity Cache cannot
-hold them: every step reads its logits and counts from HBM.
+Default workload: BASELINE.json config 2 (the north star) -- 64 rows x
+151,936 f32 logits N(0, 3^2) with 5 ids/row boosted by +8, per-row history
+counts from 1,024 Zipf(1.1) ids, presence 1.5 + repetition 1.05, T 0.7,
+top-k 20, top-p 0.8, one uniform per row.  A step is one fg_sampler_hip_sample
+call over one batch (one kernel launch; two for whole-row nucleus batches).
+Inputs are generated on the device with torch (synthetic, same shapes and
+distributions as the configs) and rotated over >= 4 GB of distinct batches so
+the 256 MB Infinity Cache cannot hold them: every step reads its logits and
+counts from HBM.
 
-Output: one JSON line (see the repository's bench contract), with
-`roofline` (dominant kernel: algorithmic bytes / HIP-event launch time vs the
-8 TB/s HBM peak) and `cpu_baseline` (the C oracle on the host cores over a
-bounded sample of the same batch).
+`--config N` times the other configurations of BASELINE.json the same way
+(1: one greedy row; 3: 256 rows, whole-row nucleus; 4: 128 rows, quantised
+logits, greedy or sampled; 5: 1,024 rows with top-20 log-probs).  The driver
+runs the default.
+
+Output: one JSON line (see the repository's bench contract), with `roofline`
+(dominant kernel: algorithmic bytes / HIP-event launch time vs the 8 TB/s HBM
+peak) and, for config 2, `cpu_baseline` (the C oracle on the host cores over
+a bounded sample of the same batch).
 """
 from __future__ import annotations
 
@@ -33,31 +40,103 @@ METRIC = "sampled rows/sec @ vocab 151,936, batch 64; achieved HBM GB/s vs peak"
 TRAFFIC_FILE = ROOT / "profiles" / "sample_rows_config2_traffic.json"
 
 
-def make_sets(torch, dev, nsets, seed=1002):
-    """Device-side synthetic batches of config 2."""
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
+def cfg(fg_hip, t, p, k, pres=0.0, freq=0.0, rep=1.0):
+    return fg_hip.make_config(t, p, k, presence=pres, frequency=freq, repetition=rep)
+
+
+def zipf_counts(torch, g, dev, rows, draws, perm):
+    """Per-row u32 counts of `draws` Zipf(1.1) token ids (rank -> id by a
+    permutation), as the configs' history tables."""
     ranks = torch.arange(1, VOCAB + 1, device=dev, dtype=torch.float64)
     zipf = ranks.pow(-1.1)
     zipf = (zipf / zipf.sum()).float()
-    logits, counts, uniforms = [], [], []
-    for _ in range(nsets):
-        x = torch.randn((ROWS, VOCAB), generator=g, device=dev) * 3.0
-        boost = torch.randint(0, VOCAB, (ROWS, 5), generator=g, device=dev)
-        x.scatter_add_(1, boost, torch.full((ROWS, 5), 8.0, device=dev))
+    hist = perm[torch.multinomial(zipf.expand(rows, VOCAB), draws, replacement=True, generator=g)]
+    c = torch.zeros((rows, VOCAB), dtype=torch.int32, device=dev)
+    c.scatter_add_(1, hist, torch.ones_like(hist, dtype=torch.int32))
+    return c
+
+
+class Workload:
+    """One BASELINE.json configuration: row count, per-row controls, input
+    generator and the algorithmic bytes of one step."""
+
+    def __init__(self, cid, fg_hip, sampled=True):
+        self.cid = cid
+        self.flags = 0
+        self.logprobs = 0
+        self.penalised_rows = None
+        if cid == 1:
+            self.rows = 1
+            self.configs = [cfg(fg_hip, 0.0, 1.0, 1, rep=1.05)]
+            self.name = "config 1: 1 row x 151,936, repetition 1.05 over 64 history ids, greedy"
+        elif cid == 2:
+            self.rows = ROWS
+            self.configs = [cfg(fg_hip, 0.7, 0.8, 20, pres=1.5, rep=1.05)] * ROWS
+            self.name = ("config 2: 64 rows x 151,936 f32 logits, presence 1.5 + repetition "
+                         "1.05 over 1,024 Zipf(1.1) history ids, T 0.7, top-k 20, top-p 0.8")
+        elif cid == 3:
+            self.rows = 256
+            self.configs = [cfg(fg_hip, 1.0, 0.95, 0, pres=0.5, freq=0.3)] * 256
+            self.flags = fg_hip.ALLOW_FULL_VOCAB
+            self.name = ("config 3: 256 rows x 151,936, 2*Student-t(3), presence 0.5 + frequency "
+                         "0.3 over 8,192 Zipf history ids, T 1.0, top-p 0.95 over the whole row")
+        elif cid == 4:
+            self.rows = 128
+            self.penalised_rows = 64
+            mk = ((lambda rep: cfg(fg_hip, 0.8, 0.9, 50, rep=rep)) if sampled
+                  else (lambda rep: cfg(fg_hip, 0.0, 1.0, 1, rep=rep)))
+            self.configs = [mk(1.1)] * 64 + [mk(1.0)] * 64
+            self.name = ("config 4: 128 rows x 151,936 quantised logits, rows 0-63 repetition 1.1 "
+                         "over 256 history ids, " + ("top-k 50, top-p 0.9" if sampled else "greedy"))
+        elif cid == 5:
+            self.rows = 1024
+            self.configs = [cfg(fg_hip, 0.6, 0.95, 64, pres=1.0, freq=0.2, rep=1.05)] * 1024
+            self.logprobs = 20
+            self.name = ("config 5: 1,024 rows x 151,936, N(0,2^2)/N(0,6^2), presence 1.0 + "
+                         "frequency 0.2 + repetition 1.05 over 32,768 Zipf history ids, T 0.6, "
+                         "top-k 64, top-p 0.95, top-20 log-probs")
+        else:
+            raise SystemExit(f"bench.py: unknown --config {cid}")
+        # Algorithmic bytes: 4 B logit for every element, 4 B count for rows
+        # with penalties, plus the per-row outputs of config 5.
+        pen = self.rows if self.penalised_rows is None else self.penalised_rows
+        self.alg_bytes = 4 * VOCAB * self.rows + 4 * VOCAB * pen
+        if cid == 5:
+            self.alg_bytes += self.rows * (4 + 4 + 20 * 8)
+
+    def make(self, torch, dev, g):
+        """One device batch: (logits, counts, uniforms)."""
+        rows = self.rows
         perm = torch.randperm(VOCAB, generator=g, device=dev)
-        hist = perm[torch.multinomial(zipf.expand(ROWS, VOCAB), 1024, replacement=True, generator=g)]
-        c = torch.zeros((ROWS, VOCAB), dtype=torch.int32, device=dev)
-        c.scatter_add_(1, hist, torch.ones_like(hist, dtype=torch.int32))
-        u = torch.rand(ROWS, generator=g, device=dev)
-        logits.append(x.contiguous())
-        counts.append(c.contiguous())
-        uniforms.append(u)
-    return logits, counts, uniforms
-
-
-def configs(fg_hip):
-    return [fg_hip.make_config(0.7, 0.8, 20, presence=1.5, repetition=1.05)] * ROWS
+        if self.cid in (1, 2):
+            x = torch.randn((rows, VOCAB), generator=g, device=dev) * 3.0
+            if self.cid == 2:
+                boost = torch.randint(0, VOCAB, (rows, 5), generator=g, device=dev)
+                x.scatter_add_(1, boost, torch.full((rows, 5), 8.0, device=dev))
+                c = zipf_counts(torch, g, dev, rows, 1024, perm)
+            else:
+                ids = torch.randint(0, VOCAB, (rows, 64), generator=g, device=dev)
+                c = torch.zeros((rows, VOCAB), dtype=torch.int32, device=dev)
+                c.scatter_add_(1, ids, torch.ones_like(ids, dtype=torch.int32))
+        elif self.cid == 3:
+            z = torch.randn((rows, VOCAB), generator=g, device=dev)
+            chi = torch.distributions.Chi2(torch.tensor(3.0, device=dev)).sample((rows, VOCAB))
+            x = 2.0 * z / torch.sqrt(chi / 3.0)
+            c = zipf_counts(torch, g, dev, rows, 8192, perm)
+        elif self.cid == 4:
+            x = (torch.randn((rows, VOCAB), generator=g, device=dev) * 3.0 / 0.25).round() * 0.25
+            x = x.clamp(-16.0, 16.0)
+            spike = torch.randint(0, VOCAB, (rows, 1), generator=g, device=dev)
+            x.scatter_(1, spike, torch.full((rows, 1), 20.0, device=dev))
+            ids = torch.randint(0, VOCAB, (rows, 256), generator=g, device=dev)
+            c = torch.zeros((rows, VOCAB), dtype=torch.int32, device=dev)
+            c.scatter_add_(1, ids, torch.ones_like(ids, dtype=torch.int32))
+        else:
+            sig = torch.where(torch.arange(rows, device=dev) % 2 == 0, 2.0, 6.0).unsqueeze(1)
+            x = torch.randn((rows, VOCAB), generator=g, device=dev) * sig
+            c = zipf_counts(torch, g, dev, rows, 32768, perm)
+        u = torch.rand(rows, generator=g, device=dev)
+        return x.float().contiguous(), c.contiguous(), u
 
 
 def cpu_baseline(x, c, u, gpu_tokens, budget_s):
@@ -65,12 +144,11 @@ def cpu_baseline(x, c, u, gpu_tokens, budget_s):
     host's cores over a bounded sample of batch 0; also cross-checks the GPU's
     tokens for that batch."""
     sys.path.insert(0, str(ROOT / "oracle"))
-    import numpy as np
     import oracle_ffi as O
 
-    cfg = [dict(temperature=0.7, top_p=0.8, top_k=20, presence=1.5, frequency=0.0,
-                repetition=1.05)] * ROWS
-    ref = O.sample_rows(cfg, x, u, counts=c, threads=1)
+    cfgs = [dict(temperature=0.7, top_p=0.8, top_k=20, presence=1.5, frequency=0.0,
+                 repetition=1.05)] * ROWS
+    ref = O.sample_rows(cfgs, x, u, counts=c, threads=1)
     same = (ref["token"] == gpu_tokens) | (ref["margin"] < 1e-6)
     parity = f"{int(same.sum())}/{ROWS} rows match the oracle (bit-exact ids, 1e-6 boundary clause)"
 
@@ -78,7 +156,7 @@ def cpu_baseline(x, c, u, gpu_tokens, budget_s):
         rows = 0
         t0 = time.perf_counter()
         while True:
-            O.sample_rows(cfg, x, u, counts=c, threads=threads)
+            O.sample_rows(cfgs, x, u, counts=c, threads=threads)
             rows += ROWS
             el = time.perf_counter() - t0
             if el >= budget:
@@ -101,6 +179,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--config", type=int, default=2, help="BASELINE.json configuration (1-5)")
+    ap.add_argument("--greedy", action="store_true", help="config 4: the greedy run")
     ap.add_argument("--set-gb", type=float, default=4.0, help="distinct input bytes to rotate over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -129,20 +209,29 @@ def main():
         print(json.dumps({"calibration": "copy", "bytes_read": src.numel() * 4,
                           "bytes_written": dst.numel() * 4, "launches": args.steps}))
         return
-    set_bytes = ROWS * ALG_BYTES_PER_ROW
-    nsets = max(4, int(args.set_gb * 1e9 / set_bytes + 0.999))
-    logits, counts, uniforms = make_sets(torch, dev, nsets)
+
+    w = Workload(args.config, fg_hip, sampled=not args.greedy)
+    batch_bytes = 8 * VOCAB * w.rows
+    nsets = max(2, int(args.set_gb * 1e9 / batch_bytes + 0.999))
+    g = torch.Generator(device=dev)
+    g.manual_seed(1000 + args.config)
+    sets = [w.make(torch, dev, g) for _ in range(nsets)]
     torch.cuda.synchronize()
 
-    sampler = fg_hip.HipSampler(VOCAB, ROWS)
+    sampler = fg_hip.HipSampler(VOCAB, w.rows)
     stream = torch.cuda.current_stream()
-    sampler.set_configs(configs(fg_hip), stream=stream.cuda_stream)
-    tokens = torch.empty((nsets, ROWS), dtype=torch.int32, device=dev)
-    status = torch.empty((nsets, ROWS), dtype=torch.int32, device=dev)
+    sampler.set_configs(w.configs, flags=w.flags, stream=stream.cuda_stream)
+    tokens = torch.empty((nsets, w.rows), dtype=torch.int32, device=dev)
+    status = torch.empty((nsets, w.rows), dtype=torch.int32, device=dev)
+    L = w.logprobs
+    lpv = torch.empty((w.rows, max(L, 1)), dtype=torch.float32, device=dev)
+    lpi = torch.empty((w.rows, max(L, 1)), dtype=torch.int32, device=dev)
 
     def step(i):
         k = i % nsets
-        sampler.sample(logits[k], uniforms[k], tokens[k], counts=counts[k], row_status=status[k],
+        x, c, u = sets[k]
+        sampler.sample(x, u, tokens[k], counts=c, row_status=status[k], logprobs=L,
+                       logprob_values=lpv if L else None, logprob_ids=lpi if L else None,
                        stream=stream.cuda_stream)
 
     for i in range(args.warmup):
@@ -159,16 +248,18 @@ def main():
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end)
     per_launch_s = ms / 1e3 / args.steps
-    rows_per_s = ROWS * args.steps / (ms / 1e3)
-    achieved = set_bytes / per_launch_s / 1e9
-    assert int((status != 0).sum()) == 0, "rows reported errors"
+    rows_per_s = w.rows * args.steps / (ms / 1e3)
+    achieved = w.alg_bytes / per_launch_s / 1e9
+    bad = int((status != 0).sum())
+    assert bad == 0, f"{bad} rows reported errors"
 
     traffic = None
-    if TRAFFIC_FILE.exists():
+    if args.config == 2 and TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
 
     line = {
-        "metric": METRIC,
+        "metric": METRIC if args.config == 2 else
+        f"sampled rows/sec @ vocab 151,936, batch {w.rows}; achieved HBM GB/s vs peak",
         "value": round(rows_per_s, 1),
         "unit": "rows/s",
         "n_gpus": 1,
@@ -179,23 +270,23 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (device-generated config-2 batches, rotated over "
-                f"{nsets} distinct sets = {nsets * set_bytes / 1e9:.2f} GB)",
-        "config": {"workload": "config 2: 64 rows x 151,936 f32 logits, presence 1.5 + repetition "
-                               "1.05 over 1,024 Zipf(1.1) history ids, T 0.7, top-k 20, top-p 0.8",
-                   "rows": ROWS, "vocab": VOCAB, "global_batch": ROWS, "parallelism": "single GPU"},
+        "data": f"synthetic (device-generated config-{args.config} batches, rotated over "
+                f"{nsets} distinct sets = {nsets * batch_bytes / 1e9:.2f} GB)",
+        "config": {"workload": w.name, "rows": w.rows, "vocab": VOCAB, "global_batch": w.rows,
+                   "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": "fg::sample_rows_kernel<true>",
-                     "algorithmic_bytes_per_launch": set_bytes,
+                     "kernel": "fg::sample_rows_kernel",
+                     "algorithmic_bytes_per_launch": w.alg_bytes,
                      "launch_us": round(per_launch_s * 1e6, 3)},
         "wall_s": round(wall, 3),
     }
-    if not args.no_cpu:
+    if args.config == 2 and not args.no_cpu:
+        x, c, u = sets[0]
         g_tok = tokens[0].cpu().numpy().view("uint32")
-        cpu, parity = cpu_baseline(logits[0].cpu().numpy(), counts[0].cpu().numpy().view("uint32"),
-                                   uniforms[0].cpu().numpy(), g_tok, args.cpu_seconds)
+        cpu, parity = cpu_baseline(x.cpu().numpy(), c.cpu().numpy().view("uint32"),
+                                   u.cpu().numpy(), g_tok, args.cpu_seconds)
         line["cpu_baseline"] = cpu
         line["parity"] = parity
     print(json.dumps(line))
