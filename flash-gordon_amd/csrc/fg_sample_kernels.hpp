@@ -370,7 +370,7 @@ __device__ __forceinline__ Mass wave_mass_combine(double m, double z, double e) 
 // whole-row nucleus.  Writes token, logit, status and log-probs.
 __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint32_t row,
                                   uint64_t fin, uint64_t gbest, double m, double z, Mass zs,
-                                  const float* lrow, const uint32_t* crow, bool pen) {
+                                  const float* lrow, const uint32_t* crow, bool pen, float u) {
   const uint32_t lane = lane_id();
   const bool greedy = p.temperature == 0.0f;
   const uint32_t L = a.logprobs;
@@ -384,10 +384,16 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
   if (greedy) {
     // src/output.c:560-599 / 728-741: a non-finite winner is an error.
     const uint32_t id = greedy_id(gbest);
+    const uint32_t hi = static_cast<uint32_t>(gbest >> 32);
     float v = -INFINITY;
     if (gbest != 0ull && id < a.vocab) {
-      v = lrow[id];
-      if (pen) v = penalise(v, crow[id], p.presence, p.frequency, p.repetition);
+      if (hi != 0xffffffffu && hi != 0x80000000u) {
+        v = key_to_float(hi);  // the penalised value itself
+      } else {
+        // Non-finite, or a zero whose sign the composite folded: re-read.
+        v = lrow[id];
+        if (pen) v = penalise(v, crow[id], p.presence, p.frequency, p.repetition);
+      }
     }
     token_logit = v;
     if (gbest == 0ull || !is_finite_bits(__float_as_uint(v)))
@@ -425,8 +431,10 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
       if (!(sum > 0.0) || !isfinite(sum)) {
         status = kStFormat;
       } else {
-        const double cum = wave_prefix_sum_f64(e / sum);
-        const uint64_t hit = ballot(live && cum >= static_cast<double>(p.top_p));
+        // Running probability ecum / sum against top_p, as ecum >= top_p * sum
+        // (the reference sums the quotients; both differ by rounding only).
+        const double target = static_cast<double>(p.top_p) * sum;
+        const uint64_t hit = ballot(live && ecum >= target);
         uint32_t cutoff = hit ? static_cast<uint32_t>(__builtin_ctzll(hit)) + 1u : limit;
         // A deeper cut, or a list that ends on zeros (where key order, +0
         // above -0, and value order, 0 == -0, may keep different entries),
@@ -435,12 +443,11 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
         const bool zero_edge = edge_key == 0x7fffffffu || edge_key == 0x80000000u;
         // So is a cut that the mass's error bound could move: the positions
         // either side of the cut must clear top_p by twice the bound.
-        const double gap = lane < cutoff ? fabs(cum - static_cast<double>(p.top_p)) : INFINITY;
+        const double gap = lane < cutoff ? fabs(ecum - target) / sum : INFINITY;
         const bool close = -wave_max_f64(-gap) <= 2.0 * bound;
         if (nuc && !whole_row_listed && (hit == 0ull || zero_edge || close)) status = kStLimit;
-        const double t = static_cast<double>(p.temperature);
-        const double vmax_t = vmax / t;
-        const double te = lane < cutoff ? exp(v / t - vmax_t) : 0.0;
+        const double inv_t = 1.0 / static_cast<double>(p.temperature);
+        const double te = lane < cutoff ? exp((v - vmax) * inv_t) : 0.0;
         const double tcum = wave_prefix_sum_f64(te);
         const double tsum = __longlong_as_double(static_cast<long long>(
             readlane64(static_cast<uint64_t>(__double_as_longlong(tcum)), cutoff - 1u)));
@@ -449,7 +456,6 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
         } else if (!(tsum > 0.0) || !isfinite(tsum)) {
           status = kStFormat;
         } else {
-          float u = a.uniforms[row];
           if (!is_finite_bits(__float_as_uint(u)) || u < 0.0f) u = 0.0f;
           if (u >= 1.0f) u = __uint_as_float(0x3f7fffffu);  // nextafterf(1, 0)
           const double draw = static_cast<double>(u) * tsum;
@@ -748,6 +754,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint32_t row = blockIdx.x / a.chunks;
   const uint32_t chunk = blockIdx.x - row * a.chunks;
   const RowParams p = a.params[row];
+  const float urow = a.uniforms[row];  // early: the row's last step needs it
   const bool greedy = p.temperature == 0.0f;
   const uint32_t L = a.logprobs;
   const bool lse = F::kLse && L != 0u;
@@ -875,7 +882,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       if (lse) lse_accumulate(m, z, s_lm[w], s_lz[w], t_eff);
       if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
     }
-    finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen);
+    finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow);
     return;
   }
 
@@ -927,9 +934,17 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     s_top[wave][lane] = acc;
     __syncthreads();
     FG_TRACE(a, 5);
+    // Waves 0 and 1 merge pairs side by side, then wave 0 merges the two.
+    if (wave < 2) {
+      const uint64_t o = s_top[wave + 2][lane];
+      if (readlane64(o, 0) > readlane64(acc, kk - 1u)) acc = wave_merge_desc(acc, o);
+    }
+    __syncthreads();
+    if (wave == 1) s_top[1][lane] = acc;
+    __syncthreads();
     if (wave == 0) {
-      fin = acc;
-      for (int w = 1; w < kWaves; w++) fin = wave_merge_desc(fin, s_top[w][lane]);
+      const uint64_t o = s_top[1][lane];
+      fin = readlane64(o, 0) > readlane64(acc, kk - 1u) ? wave_merge_desc(acc, o) : acc;
     }
   }
   if (wave != 0) return;
@@ -956,7 +971,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     zs = wave_mass_combine(lm.m, lm.z, lm.e);
   }
   FG_TRACE(a, 6);
-  finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen);
+  finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow);
   if (lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
   FG_TRACE(a, 7);
 }
