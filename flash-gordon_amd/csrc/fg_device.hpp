@@ -279,6 +279,21 @@ __device__ __forceinline__ T wave_sort_desc(T v) {
   v = bitonic_merge_stage<32>(v);
   return bitonic_merge_stage<64>(v);
 }
+// Sorts lanes [0, w) descending when every lane >= w holds 0.  After the
+// stage of width K, lanes [0, K) form a descending block, so for w <= 16 or
+// w <= 32 the later stages only reorder zeros and are skipped (10 or 15
+// steps instead of 21; the width-16 stages stay inside a DPP row).  The
+// result is a descending 64-lane sequence, zeros last.
+__device__ __forceinline__ uint64_t wave_sort_desc_first(uint64_t v, uint32_t w) {
+  v = bitonic_merge_stage<2>(v);
+  v = bitonic_merge_stage<4>(v);
+  v = bitonic_merge_stage<8>(v);
+  v = bitonic_merge_stage<16>(v);
+  if (w <= 16u) return v;
+  v = bitonic_merge_stage<32>(v);
+  if (w <= 32u) return v;
+  return bitonic_merge_stage<64>(v);
+}
 __device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t v) { return wave_sort_desc(v); }
 __device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) { return wave_sort_desc(v); }
 

@@ -252,7 +252,7 @@ __device__ __forceinline__ void top_drain(TopList& t, bool all) {
     if (x <= t.R) x = 0ull;  // beaten by a list that grew after it was staged
     if (ballot(x != 0ull) == 0ull) continue;
     FG_COUNT(all ? 3 : 0, 1ull);
-    const uint64_t sorted = wave_sort_desc(x);
+    const uint64_t sorted = wave_sort_desc_first(x, take);
     if (ballot(t.top != 0ull) == 0ull) {
       t.top = sorted;
       const uint64_t kth = readlane64(t.top, t.kk - 1u);
@@ -706,9 +706,8 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
       if (T) top_raise(st.t, key_floor(T));
       top_share(st.t, T);
       st.first = false;
-    } else {
-      top_adopt(st.t);
     }
+    top_adopt(st.t);  // the workgroup's bound (the other waves' first steps too)
     // Most steps hold no candidate once the filter has risen: one ballot on
     // the lane maxima skips the per-element staging.
     float lane_max = -INFINITY;
