@@ -144,6 +144,19 @@ fg_status fg_hip_topk_select(float* output_scores, uint32_t* output_ids,
   return FG_OK;
 }
 
+fg_status fg_hip_history_build_wire(uint32_t* counts, uint64_t counts_stride, uint32_t vocab,
+                                    const uint8_t* payloads, const uint64_t* offsets,
+                                    uint32_t rows, int32_t* row_status, uint8_t* row_slot,
+                                    void* stream, fg_error* err) {
+  if (!counts || !vocab || !payloads || !offsets || !row_status || !rows ||
+      counts_stride < vocab)
+    return arg_fail(err, "invalid output history payloads");
+  fg::history_wire_kernel<<<rows, fg::kWireBlock, 0, as_stream(stream)>>>(
+      counts, counts_stride, vocab, payloads, offsets, row_status, row_slot);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "history wire launch");
+}
+
 fg_status fg_hip_history_build(uint32_t* counts, uint64_t counts_stride, uint32_t vocab,
                                const uint32_t* ids, const uint64_t* offsets, uint32_t rows,
                                void* stream, fg_error* err) {

@@ -192,4 +192,60 @@ __global__ __launch_bounds__(256) void history_increment_kernel(uint32_t* counts
   saturating_increment(counts + static_cast<uint64_t>(r) * stride + tok);
 }
 
+// FG_MSG_OUTPUT_HISTORY payloads (src/protocol.c:1348-1366) decoded on the
+// device and turned into count tables (src/output.c:601-617), one row per
+// workgroup: validate the whole payload first, then clear the row and count.
+// A row that fails validation keeps its counts; its status says why
+// (FG_ERR_ARGUMENT: shorter than the header; FG_ERR_FORMAT: the decoder's
+// other checks).  Payload bytes are big-endian and need not be aligned.
+constexpr int kWireBlock = 1024;
+constexpr uint32_t kWireHeader = 8u;
+constexpr uint32_t kWireMaxCount = 262144u;
+constexpr uint32_t kWireMaxSlots = 2u;
+
+__device__ __forceinline__ uint32_t load_be32(const uint8_t* p) {
+  return (static_cast<uint32_t>(p[0]) << 24) | (static_cast<uint32_t>(p[1]) << 16) |
+         (static_cast<uint32_t>(p[2]) << 8) | static_cast<uint32_t>(p[3]);
+}
+
+__global__ __launch_bounds__(kWireBlock) void history_wire_kernel(
+    uint32_t* counts, uint64_t stride, uint32_t vocab, const uint8_t* payloads,
+    const uint64_t* offsets, int32_t* row_status, uint8_t* row_slot) {
+  __shared__ int32_t s_status;
+  __shared__ uint32_t s_count;
+  const uint32_t r = blockIdx.x;
+  const uint8_t* p = payloads + offsets[r];
+  const uint64_t bytes = offsets[r + 1] - offsets[r];
+  if (threadIdx.x == 0) {
+    int32_t st = 0;
+    uint32_t count = 0u;
+    if (bytes < kWireHeader) {
+      st = 2;  // FG_ERR_ARGUMENT
+    } else {
+      count = load_be32(p);
+      const uint32_t reserved = (static_cast<uint32_t>(p[5]) << 16) |
+                                (static_cast<uint32_t>(p[6]) << 8) | p[7];
+      if (reserved || p[4] >= kWireMaxSlots || count > kWireMaxCount ||
+          kWireHeader + 4ull * count != bytes)
+        st = 4;  // FG_ERR_FORMAT
+      if (row_slot) row_slot[r] = st == 0 ? p[4] : 0u;
+    }
+    s_status = st;
+    s_count = st == 0 ? count : 0u;
+  }
+  __syncthreads();
+  const uint32_t count = s_count;
+  for (uint32_t i = threadIdx.x; i < count; i += kWireBlock)
+    if (load_be32(p + kWireHeader + 4u * i) >= vocab) atomicOr(&s_status, 4);
+  __syncthreads();
+  const int32_t st = s_status;
+  if (threadIdx.x == 0) row_status[r] = st;
+  if (st != 0) return;
+  uint32_t* crow = counts + static_cast<uint64_t>(r) * stride;
+  for (uint32_t i = threadIdx.x; i < vocab; i += kWireBlock) crow[i] = 0u;
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < count; i += kWireBlock)
+    saturating_increment(crow + load_be32(p + kWireHeader + 4u * i));
+}
+
 }  // namespace fg

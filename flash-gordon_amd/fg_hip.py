@@ -36,7 +36,9 @@ EXPORTS = (
     "fg_sampler_state_init", "fg_sampler_uniform", "fg_sampler_select",
     "fg_sampler_penalties_active", "fg_sampler_apply_penalties",
     "fg_hip_apply_penalties", "fg_hip_argmax_reduce", "fg_hip_topk_select",
-    "fg_hip_history_build",
+    "fg_hip_history_build", "fg_hip_history_build_wire",
+    "fg_output_history_encode", "fg_output_history_encode_vocab",
+    "fg_output_history_decode", "fg_output_history_decode_vocab",
     "fg_sampler_hip_create", "fg_sampler_hip_destroy", "fg_sampler_hip_set_configs",
     "fg_sampler_hip_sample", "fg_sampler_hip_history_increment",
 )
@@ -71,6 +73,15 @@ class Batch(C.Structure):
     ]
 
 
+class OutputHistory(C.Structure):
+    """fg_output_history (include/fg_history.h)."""
+    _fields_ = [("tokens", C.c_void_p), ("count", C.c_uint32), ("session_slot", C.c_uint8)]
+
+
+HISTORY_HEADER_BYTES = 8
+HISTORY_Q38_VOCAB = 248320
+
+
 class FgStatusError(RuntimeError):
     def __init__(self, code: int, message: str):
         super().__init__(f"fg_status {code}: {message}")
@@ -100,6 +111,13 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_hip_argmax_reduce": (C.c_int, [P, P, P, P, u32, C.POINTER(u32), P, E]),
         "fg_hip_topk_select": (C.c_int, [P, P, P, P, u32, u32, C.POINTER(u32), P, E]),
         "fg_hip_history_build": (C.c_int, [P, u64, u32, P, P, u32, P, E]),
+        "fg_hip_history_build_wire": (C.c_int, [P, u64, u32, P, P, u32, P, P, P, E]),
+        "fg_output_history_encode": (C.c_int, [P, u32, C.POINTER(u32), C.POINTER(OutputHistory), E]),
+        "fg_output_history_encode_vocab":
+            (C.c_int, [P, u32, C.POINTER(u32), C.POINTER(OutputHistory), u32, E]),
+        "fg_output_history_decode": (C.c_int, [C.POINTER(OutputHistory), P, u32, P, u32, E]),
+        "fg_output_history_decode_vocab":
+            (C.c_int, [C.POINTER(OutputHistory), P, u32, P, u32, u32, E]),
         "fg_sampler_hip_create": (C.c_int, [C.POINTER(P), u32, u32, E]),
         "fg_sampler_hip_destroy": (None, [P]),
         "fg_sampler_hip_set_configs": (C.c_int, [P, C.POINTER(SamplerConfig), u32, u32, P, E]),
@@ -175,6 +193,51 @@ def history_build(counts, stride, vocab, ids, offsets, rows, stream=None):
     err = FgError()
     _check(lib().fg_hip_history_build(_ptr(counts), stride, vocab, _ptr(ids), _ptr(offsets),
                                       rows, _stream(stream), C.byref(err)), err)
+
+
+def history_build_wire(counts, stride, vocab, payloads, offsets, rows, row_status,
+                       row_slot=None, stream=None):
+    """fg_hip_history_build_wire: count tables from FG_MSG_OUTPUT_HISTORY payloads."""
+    err = FgError()
+    _check(lib().fg_hip_history_build_wire(_ptr(counts), stride, vocab, _ptr(payloads),
+                                           _ptr(offsets), rows, _ptr(row_status),
+                                           _ptr(row_slot), _stream(stream), C.byref(err)), err)
+
+
+def history_encode(tokens, session_slot=0, vocab=None, capacity=None):
+    """fg_output_history_encode(_vocab): the payload bytes; raises FgStatusError."""
+    import numpy as np
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    h = OutputHistory(t.ctypes.data if t.size else None, t.size, session_slot)
+    cap = capacity if capacity is not None else HISTORY_HEADER_BYTES + 4 * t.size
+    buf = (C.c_uint8 * max(cap, 1))()
+    n = C.c_uint32(0)
+    err = FgError()
+    if vocab is None:
+        st = lib().fg_output_history_encode(buf, cap, C.byref(n), C.byref(h), C.byref(err))
+    else:
+        st = lib().fg_output_history_encode_vocab(buf, cap, C.byref(n), C.byref(h), vocab,
+                                                  C.byref(err))
+    _check(st, err)
+    return bytes(buf[:n.value])
+
+
+def history_decode(payload: bytes, capacity: int, vocab=None):
+    """fg_output_history_decode(_vocab): (tokens as a list, session_slot)."""
+    import numpy as np
+    storage = np.zeros(max(capacity, 1), dtype=np.uint32)
+    h = OutputHistory()
+    src = (C.c_uint8 * max(len(payload), 1)).from_buffer_copy(payload or b"\0")
+    err = FgError()
+    sp = storage.ctypes.data if capacity else None
+    if vocab is None:
+        st = lib().fg_output_history_decode(C.byref(h), sp, capacity, src, len(payload),
+                                            C.byref(err))
+    else:
+        st = lib().fg_output_history_decode_vocab(C.byref(h), sp, capacity, src, len(payload),
+                                                  vocab, C.byref(err))
+    _check(st, err)
+    return storage[:h.count].tolist(), h.session_slot
 
 
 # ---- batched sampler -------------------------------------------------------

@@ -85,6 +85,21 @@ fg_status fg_hip_history_build(uint32_t *counts, uint64_t counts_stride, uint32_
                                const uint32_t *ids, const uint64_t *offsets,
                                uint32_t rows, void *stream, fg_error *err);
 
+/* The same count tables straight from FG_MSG_OUTPUT_HISTORY payloads
+ * (fg_history.h): row r's payload is payloads[offsets[r] .. offsets[r+1])
+ * (device memory, big-endian, any alignment).  Each payload is checked as
+ * fg_output_history_decode_vocab checks it, against `vocab`; row_status[r]
+ * gets FG_OK, FG_ERR_ARGUMENT (shorter than the header) or FG_ERR_FORMAT,
+ * and row_slot[r] (optional) the session slot.  A valid row's counts are
+ * cleared and incremented per token (saturating); an invalid row's counts
+ * are left as they were, as the reference leaves the history when decoding
+ * fails (src/runtime.c:2696-2702 then src/output.c:601-617).  Stream-ordered,
+ * no synchronisation.  Errors: null pointers, rows == 0, stride < vocab. */
+fg_status fg_hip_history_build_wire(uint32_t *counts, uint64_t counts_stride, uint32_t vocab,
+                                    const uint8_t *payloads, const uint64_t *offsets,
+                                    uint32_t rows, int32_t *row_status, uint8_t *row_slot,
+                                    void *stream, fg_error *err);
+
 /* ------------------------------------------------------------------------ */
 /* 2. Batched sampler                                                        */
 /* ------------------------------------------------------------------------ */

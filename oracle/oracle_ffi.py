@@ -228,3 +228,30 @@ def sample_rows(configs, logits, uniforms, counts=None, logprobs=0, want_penalis
     if want_penalised:
         out["penalised"] = pen
     return out
+
+
+# ---- output-history payload (restatement; pinned by tests/golden/ref_history_vectors.json) ----
+
+HISTORY_HEADER = 8
+HISTORY_MAX_COUNT = 262144  # FG_NATIVE_CONTEXT
+HISTORY_MAX_SLOTS = 2       # FG_DECODE_BATCH_MAX_SLOTS
+
+
+def history_decode(payload: bytes, capacity: int, vocab: int):
+    """fg_output_history_decode (reference src/protocol.c:1348-1366) restated:
+    returns (status, tokens, slot); status 2 = FG_ERR_ARGUMENT (shorter than
+    the header), 4 = FG_ERR_FORMAT (reserved bytes, slot, count vs context,
+    capacity and size, token range), 0 = OK."""
+    if len(payload) < HISTORY_HEADER:
+        return 2, None, None
+    count = int.from_bytes(payload[0:4], "big")
+    slot = payload[4]
+    reserved = int.from_bytes(payload[5:8], "big")
+    if (reserved or slot >= HISTORY_MAX_SLOTS or count > HISTORY_MAX_COUNT or count > capacity
+            or HISTORY_HEADER + 4 * count != len(payload)):
+        return 4, None, None
+    tokens = [int.from_bytes(payload[HISTORY_HEADER + 4 * i:HISTORY_HEADER + 4 * i + 4], "big")
+              for i in range(count)]
+    if any(t >= vocab for t in tokens):
+        return 4, None, None
+    return 0, tokens, slot

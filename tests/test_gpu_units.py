@@ -190,3 +190,62 @@ def test_history_build_matches_oracle(dev):
     with pytest.raises(fg_hip.FgStatusError) as e:
         fg_hip.history_build(d, vocab + 8, vocab, dev_u32(bad, dev), offsets, rows)
     assert e.value.code == fg_hip.FG_ERR_FORMAT
+
+
+def test_history_build_wire_matches_oracle(dev):
+    """fg_hip_history_build_wire: valid payloads (Zipf histories with repeats,
+    empty, one token, slot 1, an unaligned start) rebuild their rows; every
+    malformation the decoder checks leaves its row's counts untouched and
+    reports the decoder's status (oracle: the restated decoder, pinned to the
+    reference's compiled codec)."""
+    import struct
+    import torch
+    vocab = 151_936
+    ids = O.gen_zipf_ids(3, 2000, vocab, 1.1, 9, 9)
+
+    def wire(tokens, slot=0, count=None, reserved=b"\0\0\0"):
+        n = len(tokens) if count is None else count
+        return struct.pack(">IB", n, slot) + reserved + b"".join(struct.pack(">I", t) for t in tokens)
+
+    payloads = [
+        wire(ids[0].tolist()),                      # valid, many repeats
+        wire([]),                                   # valid, empty
+        wire([vocab - 1], slot=1),                  # valid, slot 1
+        wire(ids[1].tolist()[:777]),                # valid (starts unaligned below)
+        wire([1, 2, 3], slot=2),                    # bad slot
+        wire([1, 2, 3], reserved=b"\0\0\1"),       # reserved byte
+        wire([1, 2, 3], count=4),                   # count vs size
+        wire([1, vocab, 3]),                        # token out of range
+        b"\0\0\0",                                  # shorter than the header
+        wire(ids[2].tolist()),                      # valid
+    ]
+    blob = bytearray(b"\x5a")                       # one pad byte: payload 0 starts unaligned
+    offsets = []
+    for pl in payloads:
+        offsets.append(len(blob))
+        blob += pl
+    offsets.append(len(blob))
+    rows = len(payloads)
+    d_blob = torch.from_numpy(np.frombuffer(bytes(blob), dtype=np.uint8).copy()).to(dev)
+    d_off = torch.tensor(offsets, dtype=torch.int64, device=dev)
+    stride = vocab + 5
+    counts = torch.full((rows, stride), 77, dtype=torch.int32, device=dev)
+    status = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+    slots = torch.full((rows,), 9, dtype=torch.uint8, device=dev)
+    fg_hip.history_build_wire(counts, stride, vocab, d_blob, d_off, rows, status, slots)
+    torch.cuda.synchronize()
+    got = u32(counts)
+    st = status.cpu().numpy()
+    sl = slots.cpu().numpy()
+    for r, pl in enumerate(payloads):
+        want_st, tokens, slot = O.history_decode(pl, 1 << 20, vocab)
+        assert st[r] == want_st, f"row {r}: status {st[r]} vs {want_st}"
+        if want_st == 0:
+            want = np.bincount(np.asarray(tokens, dtype=np.int64), minlength=vocab).astype(np.uint32)
+            assert np.array_equal(got[r, :vocab], want), f"row {r}: counts"
+            assert sl[r] == slot
+        else:
+            assert (got[r, :vocab] == 77).all(), f"row {r}: counts changed"
+        assert (got[r, vocab:] == 77).all()
+    with pytest.raises(fg_hip.FgStatusError):
+        fg_hip.history_build_wire(counts, vocab - 1, vocab, d_blob, d_off, rows, status)
