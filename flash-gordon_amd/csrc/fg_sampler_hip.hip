@@ -144,6 +144,24 @@ fg_status fg_hip_topk_select(float* output_scores, uint32_t* output_ids,
   return FG_OK;
 }
 
+fg_status fg_hip_topk_reduce(float* output_scores, uint32_t* output_ids,
+                             const float* input_scores, const uint32_t* input_ids, uint32_t count,
+                             uint32_t* output_count, void* stream, fg_error* err) {
+  if (!output_scores || !output_ids || !input_scores || !count || !output_count) {
+    fg_error_set(err, FG_ERR_ARGUMENT, "invalid top-k reduction dispatch");
+    return FG_ERR_ARGUMENT;
+  }
+  const uint32_t tiles = (count + fg::kReduceTile - 1u) / fg::kReduceTile;
+  const uint32_t produced = (tiles == 1u && count < fg::kReduceKeep) ? count : tiles * fg::kReduceKeep;
+  const uint32_t per_tile = tiles == 1u ? produced : fg::kReduceKeep;
+  fg::topk_reduce_kernel<<<tiles, fg::kReduceBlock, 0, as_stream(stream)>>>(
+      output_scores, output_ids, input_scores, input_ids, count, per_tile);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(err, e, "top-k reduction launch");
+  *output_count = produced;
+  return FG_OK;
+}
+
 fg_status fg_hip_history_build_wire(uint32_t* counts, uint64_t counts_stride, uint32_t vocab,
                                     const uint8_t* payloads, const uint64_t* offsets,
                                     uint32_t rows, int32_t* row_status, uint8_t* row_slot,

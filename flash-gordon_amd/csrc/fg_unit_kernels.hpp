@@ -248,4 +248,70 @@ __global__ __launch_bounds__(kWireBlock) void history_wire_kernel(
     saturating_increment(crow + load_be32(p + kWireHeader + 4u * i));
 }
 
+// Top-512 reduction of shaders/fg_topk_reduce_v2.comp (src/vk.c:2235): per
+// 4096-element tile, the tile's entries in the greedy order of its
+// comparator (:9; padding id 0xffffffff last, non-finite first with lower id
+// first, then larger value, equal values (0 == -0) by lower id), the first
+// min(512, n) written, the rest of the 512 slots padded with (-inf,
+// 0xffffffff).  One workgroup per tile sorts (greedy composite, position)
+// pairs with a bitonic network in LDS; scores and ids are then copied from
+// the input by position, so every bit of a value (NaN payloads, -0) is kept.
+constexpr int kReduceBlock = 512;
+constexpr uint32_t kReduceTile = 4096u;
+constexpr uint32_t kReduceKeep = 512u;
+
+__global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
+    float* out_scores, uint32_t* out_ids, const float* in_scores, const uint32_t* in_ids,
+    uint32_t count, uint32_t out_per_tile) {
+  __shared__ uint64_t s_key[kReduceTile];
+  __shared__ uint16_t s_pos[kReduceTile];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t base = blockIdx.x * kReduceTile;
+  const uint32_t n = min(kReduceTile, count - base);
+  uint32_t P = 1u;
+  while (P < n) P <<= 1;
+  for (uint32_t i = tid; i < P; i += kReduceBlock) {
+    uint64_t k = 0ull;
+    if (i < n) {
+      const uint32_t id = in_ids ? in_ids[base + i] : base + i;
+      // Padding ids rank last among the entries (1) but above the fill
+      // slots of a partial tile (0), which must never reach the output.
+      k = id == kInvalidId ? 1ull : greedy_comp(in_scores[base + i], id);
+    }
+    s_key[i] = k;
+    s_pos[i] = static_cast<uint16_t>(i);
+  }
+  __syncthreads();
+  for (uint32_t k = 2u; k <= P; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
+      for (uint32_t q = tid; q < P / 2u; q += kReduceBlock) {
+        const uint32_t lo = 2u * j * (q / j) + (q % j);
+        const uint32_t hi = lo + j;
+        const uint64_t a = s_key[lo], b = s_key[hi];
+        const bool desc = (lo & k) == 0u;
+        if (desc ? a < b : a > b) {
+          s_key[lo] = b;
+          s_key[hi] = a;
+          const uint16_t t = s_pos[lo];
+          s_pos[lo] = s_pos[hi];
+          s_pos[hi] = t;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  const uint32_t valid = min(kReduceKeep, n);
+  for (uint32_t i = tid; i < out_per_tile; i += kReduceBlock) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * kReduceKeep + i;
+    if (i < valid) {
+      const uint32_t src = base + s_pos[i];
+      out_scores[o] = in_scores[src];
+      out_ids[o] = in_ids ? in_ids[src] : src;
+    } else {
+      out_scores[o] = -INFINITY;
+      out_ids[o] = kInvalidId;
+    }
+  }
+}
+
 }  // namespace fg

@@ -35,7 +35,7 @@ EXPORTS = (
     "fg_sampler_config_greedy", "fg_sampler_config_defaults", "fg_sampler_config_validate",
     "fg_sampler_state_init", "fg_sampler_uniform", "fg_sampler_select",
     "fg_sampler_penalties_active", "fg_sampler_apply_penalties",
-    "fg_hip_apply_penalties", "fg_hip_argmax_reduce", "fg_hip_topk_select",
+    "fg_hip_apply_penalties", "fg_hip_argmax_reduce", "fg_hip_topk_select", "fg_hip_topk_reduce",
     "fg_hip_history_build", "fg_hip_history_build_wire",
     "fg_output_history_encode", "fg_output_history_encode_vocab",
     "fg_output_history_decode", "fg_output_history_decode_vocab",
@@ -110,6 +110,7 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_hip_apply_penalties": (C.c_int, [P, P, u32, f32, f32, f32, P, E]),
         "fg_hip_argmax_reduce": (C.c_int, [P, P, P, P, u32, C.POINTER(u32), P, E]),
         "fg_hip_topk_select": (C.c_int, [P, P, P, P, u32, u32, C.POINTER(u32), P, E]),
+        "fg_hip_topk_reduce": (C.c_int, [P, P, P, P, u32, C.POINTER(u32), P, E]),
         "fg_hip_history_build": (C.c_int, [P, u64, u32, P, P, u32, P, E]),
         "fg_hip_history_build_wire": (C.c_int, [P, u64, u32, P, P, u32, P, P, P, E]),
         "fg_output_history_encode": (C.c_int, [P, u32, C.POINTER(u32), C.POINTER(OutputHistory), E]),
@@ -185,6 +186,16 @@ def topk_select(out_scores, out_ids, in_scores, in_ids, count, k, stream=None) -
     n = C.c_uint32(0)
     _check(lib().fg_hip_topk_select(_ptr(out_scores), _ptr(out_ids), _ptr(in_scores),
                                     _ptr(in_ids), count, k, C.byref(n), _stream(stream),
+                                    C.byref(err)), err)
+    return n.value
+
+
+def topk_reduce(out_scores, out_ids, in_scores, in_ids, count, stream=None) -> int:
+    """fg_hip_topk_reduce: sorted top-512 per 4096-value tile; returns the output count."""
+    err = FgError()
+    n = C.c_uint32(0)
+    _check(lib().fg_hip_topk_reduce(_ptr(out_scores), _ptr(out_ids), _ptr(in_scores),
+                                    _ptr(in_ids), count, C.byref(n), _stream(stream),
                                     C.byref(err)), err)
     return n.value
 

@@ -75,6 +75,20 @@ fg_status fg_hip_topk_select(float *output_scores, uint32_t *output_ids,
                              uint32_t count, uint32_t k, uint32_t *output_count,
                              void *stream, fg_error *err);
 
+/* Top-512 per 4096-value tile: output tile g holds the tile's entries in
+ * the order of shaders/fg_topk_reduce_v2.comp:9 (non-finite first, then
+ * larger score, ties to the lower id; padding id 0xffffffff last), the first
+ * min(512, n_g) of them, the rest of its 512 slots (-inf, 0xffffffff).
+ * *output_count = 512 per tile, or count when one tile holds fewer than 512.
+ * Outputs must hold *output_count entries.  in_ids == NULL means ids
+ * 0..count-1.  Errors: count == 0, null pointers ("invalid top-k reduction
+ * dispatch").  Replaces fg_vk_topk_reduce (src/vk.c:2235); the caller
+ * iterates it as the reference does (src/qsa.c:839-851). */
+fg_status fg_hip_topk_reduce(float *output_scores, uint32_t *output_ids,
+                             const float *input_scores, const uint32_t *input_ids,
+                             uint32_t count, uint32_t *output_count, void *stream,
+                             fg_error *err);
+
 /* Dense history count tables from token lists: for each row r, counts[r*stride
  * .. +vocab) is cleared and then incremented once per id in
  * ids[offsets[r] .. offsets[r+1]), saturating at UINT32_MAX.  Replaces

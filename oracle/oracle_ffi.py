@@ -255,3 +255,52 @@ def history_decode(payload: bytes, capacity: int, vocab: int):
     if any(t >= vocab for t in tokens):
         return 4, None, None
     return 0, tokens, slot
+
+
+# ---- top-512 tile reduction (restatement of shaders/fg_topk_reduce_v2.comp) ----
+
+REDUCE_TILE = 4096
+REDUCE_KEEP = 512
+
+
+def reduce_before(a: float, ai: int, b: float, bi: int) -> bool:
+    """The comparator of shaders/fg_topk_reduce_v2.comp:9 (also
+    tests/test_fg_vk.c:1223-1229): padding id 0xffffffff last; non-finite
+    first, lower id first among them; then larger value, lower id on ties."""
+    ap, bp = ai == 0xFFFFFFFF, bi == 0xFFFFFFFF
+    if ap or bp:
+        return (not ap) and bp
+    an, bn = not np.isfinite(a), not np.isfinite(b)
+    if an or bn:
+        return an if an != bn else ai < bi
+    return a > b or (a == b and ai < bi)
+
+
+def reduce_order_key(scores: np.ndarray, ids: np.ndarray):
+    """np.lexsort keys (last = primary) giving the comparator's order."""
+    s = scores.astype(np.float64)
+    pad = (ids == 0xFFFFFFFF).astype(np.int64)
+    nonfinite = ~np.isfinite(s)
+    value = np.where(nonfinite, 0.0, s)
+    return (ids.astype(np.int64), -value, (~nonfinite).astype(np.int64), pad)
+
+
+def topk_reduce_step(scores: np.ndarray, ids: np.ndarray):
+    """fg_vk_topk_reduce (src/vk.c:2235) restated: per 4096-value tile the
+    entries in comparator order, the first min(512, n) kept, the rest of the
+    512 slots (-inf, 0xffffffff); a single tile with fewer than 512 values
+    yields exactly `count` entries."""
+    count = scores.size
+    tiles = (count + REDUCE_TILE - 1) // REDUCE_TILE
+    produced = count if tiles == 1 and count < REDUCE_KEEP else tiles * REDUCE_KEEP
+    per = produced if tiles == 1 else REDUCE_KEEP
+    out_s = np.full(produced, -np.inf, dtype=np.float32)
+    out_i = np.full(produced, 0xFFFFFFFF, dtype=np.uint32)
+    for g in range(tiles):
+        s = scores[g * REDUCE_TILE:(g + 1) * REDUCE_TILE]
+        i = ids[g * REDUCE_TILE:(g + 1) * REDUCE_TILE]
+        order = np.lexsort(reduce_order_key(s, i))
+        keep = order[:min(REDUCE_KEEP, s.size, per)]
+        out_s[g * per:g * per + keep.size] = s[keep]
+        out_i[g * per:g * per + keep.size] = i[keep]
+    return out_s, out_i

@@ -249,3 +249,112 @@ def test_history_build_wire_matches_oracle(dev):
         assert (got[r, vocab:] == 77).all()
     with pytest.raises(fg_hip.FgStatusError):
         fg_hip.history_build_wire(counts, vocab - 1, vocab, d_blob, d_off, rows, status)
+
+
+def _reduce(dev, scores, ids):
+    import torch
+    n = scores.size
+    cap = ((n + 4095) // 4096) * 512
+    os_ = torch.empty(max(cap, 1), dtype=torch.float32, device=dev)
+    oi = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+    got = fg_hip.topk_reduce(os_, oi, dev_f32(scores, dev),
+                             None if ids is None else dev_u32(ids, dev), n)
+    torch.cuda.synchronize()
+    return os_.cpu().numpy()[:got], oi.cpu().numpy().view(np.uint32)[:got], got
+
+
+def test_topk_reduce_reference_chunked():
+    """tests/test_fg_vk.c:1231-1272 restated: the reference's LCG scores (with
+    0, NaN, +Inf, -Inf every 97/257/389/521 entries), ids 0..count-1, its 39
+    counts, and its checks (output count, each value equal to the input's at
+    that id, comparator order within a tile, padding past the valid entries)."""
+    import torch
+    dev = torch.device("cuda:0")
+    counts = [1, 2, 7, 63, 64, 65, 100, 127, 128, 129, 192, 320, 448, 511, 512, 513, 576, 640,
+              704, 768, 1000, 1024, 1088, 1090, 1091, 1152, 1216, 2048, 2112, 3000, 4032, 4096,
+              4097, 4160, 4224, 5000, 8000, 8192, 8200]
+    mx = counts[-1]
+    scores = np.empty(mx, dtype=np.float32)
+    seed = 12345
+    for i in range(mx):
+        seed = (seed * 1664525 + 1013904223) & 0xFFFFFFFF
+        v = np.float32(float(np.int32(np.uint32(seed >> 8)) % 2000) * 0.5)
+        if i % 97 == 0:
+            v = np.float32(0.0)
+        if i % 257 == 0:
+            v = np.float32(np.nan)
+        if i % 389 == 0:
+            v = np.float32(np.inf)
+        if i % 521 == 0:
+            v = np.float32(-np.inf)
+        scores[i] = v
+    ids = np.arange(mx, dtype=np.uint32)
+    for count in counts:
+        gs, gi, produced = _reduce(dev, scores[:count], ids[:count])
+        tiles = (count + 4095) // 4096
+        expected = count if tiles == 1 and count < 512 else tiles * 512
+        assert produced == expected, count
+        for i in range(produced):
+            g, w = divmod(i, 512)
+            remaining = max(count - g * 4096, 0)
+            valid = min(remaining, 512)
+            if w >= valid:
+                assert gs[i] == -np.inf and gi[i] == 0xFFFFFFFF, (count, i)
+            else:
+                assert gi[i] < count and gs[i].view(np.uint32) == scores[gi[i]].view(np.uint32)
+                if w + 1 < valid:
+                    assert not O.reduce_before(gs[i + 1], gi[i + 1], gs[i], gi[i]), (count, i)
+
+
+@pytest.mark.parametrize("count", [1, 511, 512, 4096, 4097, 20_000, 151_936])
+def test_topk_reduce_matches_oracle(dev, count):
+    """Bit-exact against the oracle's restatement: NaN payloads, +-Inf, +-0,
+    quantised ties, arbitrary ids with some padding ids."""
+    rng = np.random.default_rng(count)
+    s = (np.round(rng.normal(0, 3, count) * 4) / 4).astype(np.float32)
+    s[rng.random(count) < 0.01] = np.float32(np.nan)
+    s.view(np.uint32)[rng.random(count) < 0.005] = 0x7FC00123  # NaN payload
+    s[rng.random(count) < 0.005] = np.inf
+    s[rng.random(count) < 0.005] = -np.inf
+    s[rng.random(count) < 0.05] = -0.0
+    ids = rng.permutation(count * 3)[:count].astype(np.uint32)
+    ids[rng.random(count) < 0.01] = 0xFFFFFFFF
+    gs, gi, produced = _reduce(dev, s, ids)
+    ws, wi = O.topk_reduce_step(s, ids)
+    assert produced == ws.size
+    real = wi != 0xFFFFFFFF  # padding entries tie among themselves
+    assert np.array_equal(gi[real], wi[real])
+    assert np.array_equal(gs[real].view(np.uint32), ws[real].view(np.uint32))
+    assert np.array_equal(gi == 0xFFFFFFFF, ~real)
+
+
+def test_topk_reduce_ladder_gives_sorted_top512(dev):
+    """Iterated as the reference's QSA scan iterates it (src/qsa.c:839-851):
+    the final pass holds the global top-512 in comparator order."""
+    import torch
+    rng = np.random.default_rng(3)
+    count = 300_000
+    s = rng.normal(0, 1, count).astype(np.float32)
+    s[rng.integers(0, count, 50)] = np.nan
+    ids = np.arange(count, dtype=np.uint32)
+    cur_s, cur_i, n = dev_f32(s, dev), dev_u32(ids, dev), count
+    reduced = False
+    while n > 512:
+        cap = ((n + 4095) // 4096) * 512
+        ns = torch.empty(cap, dtype=torch.float32, device=dev)
+        ni = torch.empty(cap, dtype=torch.int32, device=dev)
+        n = fg_hip.topk_reduce(ns, ni, cur_s, cur_i, n)
+        cur_s, cur_i, reduced = ns, ni, True
+    assert reduced and n == 512
+    torch.cuda.synchronize()
+    got = cur_i.cpu().numpy().view(np.uint32)[:512]
+    want = np.lexsort(O.reduce_order_key(s, ids))[:512]
+    assert np.array_equal(got, ids[want])
+
+
+def test_topk_reduce_argument_errors(dev):
+    import torch
+    x = torch.zeros(8, device=dev)
+    with pytest.raises(fg_hip.FgStatusError) as e:
+        fg_hip.topk_reduce(x, x, x, None, 0)
+    assert e.value.code == fg_hip.FG_ERR_ARGUMENT

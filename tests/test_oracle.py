@@ -302,3 +302,31 @@ def test_generators_shapes_and_moments():
     top = np.sort(counts)[::-1]
     # Zipf(1.1): rank 1 carries about 1/H share, rank 2 about 2^-1.1 of rank 1.
     assert 0.4 < top[1] / top[0] < 0.55
+
+
+def test_topk_reduce_order_matches_pairwise_comparator():
+    """The oracle's lexsort order against the comparator applied pairwise
+    (insertion sort, brute force) on small tiles with NaN, +-Inf, +-0, ties
+    and padding ids."""
+    import functools
+    rng = np.random.default_rng(5)
+    for trial in range(40):
+        n = int(rng.integers(1, 40))
+        s = np.round(rng.normal(0, 2, n) * 2) / 2
+        s[rng.random(n) < 0.1] = np.nan
+        s[rng.random(n) < 0.05] = np.inf
+        s[rng.random(n) < 0.05] = -np.inf
+        s[rng.random(n) < 0.1] = -0.0
+        s = s.astype(np.float32)
+        ids = rng.choice(10_000, n, replace=False).astype(np.uint32)
+        ids[rng.random(n) < 0.1] = 0xFFFFFFFF
+        cmp = lambda x, y: -1 if O.reduce_before(s[x], ids[x], s[y], ids[y]) else (
+            1 if O.reduce_before(s[y], ids[y], s[x], ids[x]) else 0)
+        brute = sorted(range(n), key=functools.cmp_to_key(cmp))
+        got_s, got_i = O.topk_reduce_step(s, ids)
+        want_i = ids[brute][:got_i.size]
+        # padding entries tie with each other: compare the non-padding prefix exactly
+        real = want_i != 0xFFFFFFFF
+        assert np.array_equal(got_i[:real.sum()], want_i[real]), trial
+        assert np.array_equal(got_s[:real.sum()].view(np.uint32),
+                              s[brute][:got_i.size][real].view(np.uint32))
