@@ -10,6 +10,12 @@ distributions as the configs) and rotated over >= 4 GB of distinct batches so
 the 256 MB Infinity Cache cannot hold them: every step reads its logits and
 counts from HBM.
 
+`--split WAYS` (2 or 4) times instead what the output owner's GPU does per
+token in the reference's vocabulary-split greedy output: its slice of each
+row reduced to one finalist (fg_hip_output_slice_reduce) and the finalists
+of all ways combined (fg_hip_output_split_combine); the other ways'
+finalists are reduced once, untimed, as the other ranks would send them.
+
 `--config N` times the other configurations of BASELINE.json the same way
 (1: one greedy row; 3: 256 rows, whole-row nucleus; 4: 128 rows, quantised
 logits, greedy or sampled; 5: 1,024 rows with top-20 log-probs).  The driver
@@ -174,6 +180,89 @@ def cpu_baseline(x, c, u, gpu_tokens, budget_s):
     }, parity
 
 
+def split_bench(args, torch, fg_hip, dev, w, sets, nsets, batch_bytes):
+    ways, rows = args.split, w.rows
+    quarter = VOCAB // ways
+    spans = [(i * quarter, quarter if i + 1 < ways else VOCAB - i * quarter) for i in range(ways)]
+    slices = [fg_hip.OutputSlice(VOCAB, ways, f, n, rows) for f, n in spans]
+    stream = torch.cuda.current_stream()
+    sid = stream.cuda_stream
+    parts_v = torch.empty((nsets, ways, rows), dtype=torch.float32, device=dev)
+    parts_i = torch.empty((nsets, ways, rows), dtype=torch.int32, device=dev)
+    parts_s = torch.empty((nsets, ways, rows), dtype=torch.int32, device=dev)
+    for k in range(nsets):  # the other ranks' finalists, reduced once
+        for way in range(1, ways):
+            f, n = spans[way]
+            slices[way].reduce(sets[k][0][:, f:f + n], parts_v[k, way], parts_i[k, way],
+                               parts_s[k, way], stride=VOCAB, stream=sid)
+    ranks = torch.tensor([0] + [(4, 0, 1, 2)[i] for i in range(1, ways)], dtype=torch.uint8,
+                         device=dev).repeat(rows)
+    pv = torch.empty((nsets, rows, ways), dtype=torch.float32, device=dev)
+    pi = torch.empty((nsets, rows, ways), dtype=torch.int32, device=dev)
+    tokens = torch.empty((nsets, rows), dtype=torch.int32, device=dev)
+    status = torch.zeros((nsets, rows), dtype=torch.int32, device=dev)
+    own = spans[0][1]
+
+    def step(i, sid):
+        k = i % nsets
+        slices[0].reduce(sets[k][0][:, :own], parts_v[k, 0], parts_i[k, 0], parts_s[k, 0],
+                         stride=VOCAB, stream=sid)
+        fg_hip.split_combine(tokens[k], None, status[k], pv[k], pi[k], ranks, rows, ways,
+                             VOCAB, spans, stream=sid)
+
+    # The gathered [row][way] finalists are filled once from the untimed
+    # reductions plus the owner's own reduction of the same set.
+    for k in range(nsets):
+        slices[0].reduce(sets[k][0][:, :own], parts_v[k, 0], parts_i[k, 0], parts_s[k, 0],
+                         stride=VOCAB, stream=sid)
+    pv.copy_(parts_v.transpose(1, 2))
+    pi.copy_(parts_i.transpose(1, 2))
+    # Two ~5 us launches per step are shorter than their host-side call, so
+    # the timed steps are replays of a captured HIP graph of `per_graph`
+    # steps (the kernels use no memset and keep no state between calls).
+    per_graph = 100
+    steps = max(per_graph, args.steps // per_graph * per_graph)
+    for i in range(args.warmup):
+        step(i, sid)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream().cuda_stream
+        for i in range(per_graph):
+            step(i, cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps // per_graph):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end)
+    per_step_s = ms / 1e3 / steps
+    x = sets[0][0]
+    want = torch.argmax(x, dim=1)  # finite N(0, 9) rows: the argmax is unique a.s.
+    assert bool((tokens[0] == want.to(torch.int32)).all()) and int(status.sum()) == 0
+    alg = 4 * own * rows
+    print(json.dumps({
+        "metric": f"split-output owner steps/sec ({ways}-way, vocab {VOCAB}, batch {rows})",
+        "value": round(1.0 / per_step_s, 1), "unit": "steps/s", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms / steps, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": f"synthetic (config-{args.config} logits, {nsets} rotated sets)",
+        "config": {"workload": f"split{ways}-owner-{w.name}", "rows": rows, "vocab": VOCAB,
+                   "slice_rows": own, "parallelism": "single GPU (one rank's share)"},
+        "roofline": {"bound": "hbm", "achieved": round(alg / per_step_s / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(alg / per_step_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "fg::slice_finalist_kernel + fg::split_combine_kernel",
+                     "algorithmic_bytes_per_launch": alg,
+                     "launch_us": round(per_step_s * 1e6, 3)},
+        "wall_s": round(wall, 3)}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,6 +273,8 @@ def main():
     ap.add_argument("--set-gb", type=float, default=4.0, help="distinct input bytes to rotate over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--split", type=int, default=0, choices=(0, 2, 4),
+                    help="time the owner's side of the vocabulary-split greedy output")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 1 GiB device copy (the rocprof FETCH/WRITE_SIZE reference)")
     args = ap.parse_args()
@@ -217,6 +308,9 @@ def main():
     g.manual_seed(1000 + args.config)
     sets = [w.make(torch, dev, g) for _ in range(nsets)]
     torch.cuda.synchronize()
+
+    if args.split:
+        return split_bench(args, torch, fg_hip, dev, w, sets, nsets, batch_bytes)
 
     sampler = fg_hip.HipSampler(VOCAB, w.rows)
     stream = torch.cuda.current_stream()

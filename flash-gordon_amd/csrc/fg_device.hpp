@@ -322,6 +322,14 @@ __device__ __forceinline__ void wave_merge_desc2(uint64_t& a0, uint64_t b0, uint
   a1 = x1;
 }
 
+// Waits until this wave's memory operations have completed; the signal
+// fences keep the compiler from moving memory operations across the wait.
+__device__ __forceinline__ void wait_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // ---- wave reductions and scans ------------------------------------------------
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {

@@ -127,13 +127,6 @@ __device__ __forceinline__ double load_coherent_f64(const double* p) {
   return __longlong_as_double(
       static_cast<long long>(load_coherent(reinterpret_cast<const uint64_t*>(p))));
 }
-// Waits until this wave's memory operations have completed; the signal
-// fences keep the compiler from moving memory operations across the wait.
-__device__ __forceinline__ void wait_memory() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // ---- per-wave top list ------------------------------------------------------
 //

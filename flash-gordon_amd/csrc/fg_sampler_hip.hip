@@ -9,6 +9,7 @@
 #include "fg_sampler_hip.h"
 #include "fg_nucleus_kernels.hpp"
 #include "fg_sample_kernels.hpp"
+#include "fg_split_kernels.hpp"
 #include "fg_unit_kernels.hpp"
 
 namespace {
@@ -160,6 +161,94 @@ fg_status fg_hip_topk_reduce(float* output_scores, uint32_t* output_ids,
   if (e != hipSuccess) return hip_fail(err, e, "top-k reduction launch");
   *output_count = produced;
   return FG_OK;
+}
+
+struct fg_hip_output_slice {
+  uint32_t vocab, ways, first_row, rows, max_batch;
+  unsigned long long* d_keys;  // per batch row; zero between calls
+  uint32_t* d_arrivals;        // per batch row; zero between calls
+};
+
+fg_status fg_hip_output_slice_create(fg_hip_output_slice** out, uint32_t vocab, uint32_t ways,
+                                     uint32_t first_row, uint32_t rows,
+                                     uint32_t max_batch_rows, fg_error* err) {
+  if (out) *out = nullptr;
+  if (!out || !vocab || vocab == UINT32_MAX || !rows || first_row >= vocab ||
+      rows > vocab - first_row || (ways != 2u && ways != 4u) || !max_batch_rows ||
+      max_batch_rows > 65535u)
+    return arg_fail(err, "invalid output slice arguments");
+  fg_hip_output_slice* s = static_cast<fg_hip_output_slice*>(calloc(1, sizeof(*s)));
+  if (!s) {
+    fg_error_set(err, FG_ERR_OOM, "output slice");
+    return FG_ERR_OOM;
+  }
+  *s = {vocab, ways, first_row, rows, max_batch_rows, nullptr, nullptr};
+  hipError_t e = hipMalloc(&s->d_keys, sizeof(unsigned long long) * max_batch_rows);
+  if (e == hipSuccess) e = hipMalloc(&s->d_arrivals, sizeof(uint32_t) * max_batch_rows);
+  if (e == hipSuccess) e = hipMemset(s->d_keys, 0, sizeof(unsigned long long) * max_batch_rows);
+  if (e == hipSuccess) e = hipMemset(s->d_arrivals, 0, sizeof(uint32_t) * max_batch_rows);
+  if (e != hipSuccess) {
+    fg_hip_output_slice_destroy(s);
+    return hip_fail(err, e, "output slice workspace");
+  }
+  *out = s;
+  return FG_OK;
+}
+
+void fg_hip_output_slice_destroy(fg_hip_output_slice* s) {
+  if (!s) return;
+  (void)hipFree(s->d_keys);
+  (void)hipFree(s->d_arrivals);
+  free(s);
+}
+
+uint32_t fg_hip_output_slice_ways(const fg_hip_output_slice* s) { return s ? s->ways : 0u; }
+
+fg_status fg_hip_output_slice_reduce(fg_hip_output_slice* s, const float* logits,
+                                     uint64_t stride, uint32_t batch_rows, float* values,
+                                     uint32_t* ids, int32_t* row_status, void* stream,
+                                     fg_error* err) {
+  if (!s || !logits || !values || !ids || !row_status || !batch_rows ||
+      batch_rows > s->max_batch || stride < s->rows)
+    return arg_fail(err, "invalid output slice run arguments");
+  const dim3 grid((s->rows + fg::kSliceChunk - 1u) / fg::kSliceChunk, batch_rows);
+  if (aligned16(logits) && stride % 4u == 0u && s->rows % 4u == 0u)
+    fg::slice_finalist_kernel<true><<<grid, fg::kSliceBlock, 0, as_stream(stream)>>>(
+        values, ids, row_status, logits, stride, s->first_row, s->rows, s->d_keys,
+        s->d_arrivals);
+  else
+    fg::slice_finalist_kernel<false><<<grid, fg::kSliceBlock, 0, as_stream(stream)>>>(
+        values, ids, row_status, logits, stride, s->first_row, s->rows, s->d_keys,
+        s->d_arrivals);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "output slice launch");
+}
+
+fg_status fg_hip_output_split_combine(uint32_t* tokens, float* logits_out, int32_t* row_status,
+                                      const float* part_values, const uint32_t* part_ids,
+                                      const uint8_t* part_ranks, uint32_t rows, uint32_t ways,
+                                      uint32_t vocab, const uint32_t* span_first,
+                                      const uint32_t* span_rows, void* stream, fg_error* err) {
+  if (!tokens || !row_status || !part_values || !part_ids || !part_ranks || !rows ||
+      (ways != 2u && ways != 4u) || !vocab || !span_first || !span_rows)
+    return arg_fail(err, "invalid output split combine arguments");
+  static const uint32_t kRanks[fg::kSplitWaysMax] = {4u, 0u, 1u, 2u};
+  fg::SplitSpans spans{};
+  uint64_t cursor = 0;
+  for (uint32_t w = 0; w < ways; w++) {
+    if (span_first[w] != cursor || !span_rows[w])
+      return arg_fail(err, "invalid output split combine arguments");
+    cursor += span_rows[w];
+    spans.first[w] = span_first[w];
+    spans.rows[w] = span_rows[w];
+    spans.rank[w] = kRanks[w];
+  }
+  if (cursor != vocab) return arg_fail(err, "invalid output split combine arguments");
+  fg::split_combine_kernel<<<(rows + 255u) / 256u, 256, 0, as_stream(stream)>>>(
+      tokens, logits_out, row_status, part_values, part_ids, part_ranks, rows, ways, vocab,
+      spans);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "output split combine launch");
 }
 
 fg_status fg_hip_history_build_wire(uint32_t* counts, uint64_t counts_stride, uint32_t vocab,

@@ -41,6 +41,10 @@ EXPORTS = (
     "fg_output_history_decode", "fg_output_history_decode_vocab",
     "fg_sampler_hip_create", "fg_sampler_hip_destroy", "fg_sampler_hip_set_configs",
     "fg_sampler_hip_sample", "fg_sampler_hip_history_increment",
+    "fg_output_better", "fg_output_combine", "fg_output_split_way_for_rank",
+    "fg_output_split_rank", "fg_output_split_span", "fg_output_split_combine_finalists",
+    "fg_hip_output_slice_create", "fg_hip_output_slice_destroy", "fg_hip_output_slice_ways",
+    "fg_hip_output_slice_reduce", "fg_hip_output_split_combine",
 )
 
 
@@ -124,6 +128,19 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_sampler_hip_set_configs": (C.c_int, [P, C.POINTER(SamplerConfig), u32, u32, P, E]),
         "fg_sampler_hip_sample": (C.c_int, [P, C.POINTER(Batch), P, E]),
         "fg_sampler_hip_history_increment": (C.c_int, [P, P, u64, P, P, u32, P, E]),
+        "fg_output_better": (C.c_bool, [f32, u32, f32, u32]),
+        "fg_output_combine": (None, [f32, u32, f32, u32, C.POINTER(f32), C.POINTER(u32)]),
+        "fg_output_split_way_for_rank": (C.c_bool, [u32, u32, C.POINTER(u32)]),
+        "fg_output_split_rank": (u32, [u32, u32]),
+        "fg_output_split_span": (None, [u32, u32, C.POINTER(u32), C.POINTER(u32)]),
+        "fg_output_split_combine_finalists":
+            (C.c_int, [u32, f32, u32, P, P, P, u32, C.POINTER(u32), C.POINTER(f32), E]),
+        "fg_hip_output_slice_create": (C.c_int, [C.POINTER(P), u32, u32, u32, u32, u32, E]),
+        "fg_hip_output_slice_destroy": (None, [P]),
+        "fg_hip_output_slice_ways": (u32, [P]),
+        "fg_hip_output_slice_reduce": (C.c_int, [P, P, u64, u32, P, P, P, P, E]),
+        "fg_hip_output_split_combine":
+            (C.c_int, [P, P, P, P, P, P, u32, u32, u32, P, P, P, E]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -249,6 +266,60 @@ def history_decode(payload: bytes, capacity: int, vocab=None):
                                                   vocab, C.byref(err))
     _check(st, err)
     return storage[:h.count].tolist(), h.session_slot
+
+
+# ---- vocabulary-split greedy output ----------------------------------------
+
+def split_span(ways: int, way: int) -> tuple[int, int]:
+    """fg_output_split_span: (first_row, rows)."""
+    first, rows = C.c_uint32(0), C.c_uint32(0)
+    lib().fg_output_split_span(ways, way, C.byref(first), C.byref(rows))
+    return first.value, rows.value
+
+
+def split_combine(tokens, logits_out, row_status, part_values, part_ids, part_ranks, rows,
+                  ways, vocab, spans, stream=None):
+    """fg_hip_output_split_combine; spans = [(first, rows)] by way."""
+    first = (C.c_uint32 * len(spans))(*[f for f, _ in spans])
+    count = (C.c_uint32 * len(spans))(*[r for _, r in spans])
+    err = FgError()
+    _check(lib().fg_hip_output_split_combine(
+        _ptr(tokens), _ptr(logits_out), _ptr(row_status), _ptr(part_values), _ptr(part_ids),
+        _ptr(part_ranks), rows, ways, vocab, first, count, _stream(stream), C.byref(err)), err)
+
+
+class OutputSlice:
+    """Owns an fg_hip_output_slice (vocabulary rows [first_row, first_row + rows))."""
+
+    def __init__(self, vocab, ways, first_row, rows, max_batch_rows):
+        self._lib = lib()
+        err = FgError()
+        h = C.c_void_p()
+        _check(self._lib.fg_hip_output_slice_create(C.byref(h), vocab, ways, first_row, rows,
+                                                    max_batch_rows, C.byref(err)), err)
+        self.handle, self.first_row, self.rows = h, first_row, rows
+
+    def close(self):
+        if self.handle:
+            self._lib.fg_hip_output_slice_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def ways(self) -> int:
+        return self._lib.fg_hip_output_slice_ways(self.handle)
+
+    def reduce(self, logits, values, ids, row_status, batch_rows=None, stride=None, stream=None):
+        batch_rows = batch_rows if batch_rows is not None else logits.shape[0]
+        stride = stride if stride is not None else logits.stride(0)
+        err = FgError()
+        _check(self._lib.fg_hip_output_slice_reduce(
+            self.handle, _ptr(logits), stride, batch_rows, _ptr(values), _ptr(ids),
+            _ptr(row_status), _stream(stream), C.byref(err)), err)
 
 
 # ---- batched sampler -------------------------------------------------------

@@ -187,6 +187,53 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip *sampler, uint32_t *co
                                            const int32_t *row_status, uint32_t rows,
                                            void *stream, fg_error *err);
 
+/* ---- vocabulary-split greedy output (fg_output_split.h has the layout) ----
+ * A rank holding vocabulary rows [first_row, first_row + rows) of the LM head
+ * reduces its logits to one (value, id) finalist per decode row; the output
+ * owner gathers the finalists and combines them.  Greedy only, as in the
+ * reference (src/runtime.c:2399-2401). */
+typedef struct fg_hip_output_slice fg_hip_output_slice;
+
+/* Mirrors fg_output_slice_create (src/output.c:234-258) without the model:
+ * `vocab` is the full vocabulary, `ways` 2 or 4, the slice non-empty and
+ * inside [0, vocab), and `max_batch_rows` (1..65535) the most decode rows
+ * one call reduces.  FG_ERR_ARGUMENT ("invalid output slice arguments") otherwise;
+ * FG_ERR_OOM when the workspace cannot be allocated. */
+fg_status fg_hip_output_slice_create(fg_hip_output_slice **out, uint32_t vocab, uint32_t ways,
+                                     uint32_t first_row, uint32_t rows,
+                                     uint32_t max_batch_rows, fg_error *err);
+void fg_hip_output_slice_destroy(fg_hip_output_slice *slice);
+/* ways of the slice, 0 for NULL (fg_output_slice_ways, src/output.c:336). */
+uint32_t fg_hip_output_slice_ways(const fg_hip_output_slice *slice);
+
+/* The reduction half of fg_output_slice_run (src/output.c:341-363) for
+ * batch_rows decode rows: logits[r*stride + i], i < rows, is the logit of
+ * vocabulary id first_row + i.  values[r], ids[r] receive the row's best
+ * (value, id) in fg_output_better's order; row_status[r] is FG_OK, or
+ * FG_ERR_MISMATCH when that value is non-finite ("invalid output slice
+ * finalist").  One launch; calls on one slice must not overlap (they share
+ * its workspace). */
+fg_status fg_hip_output_slice_reduce(fg_hip_output_slice *slice, const float *logits,
+                                     uint64_t stride, uint32_t batch_rows, float *values,
+                                     uint32_t *ids, int32_t *row_status, void *stream,
+                                     fg_error *err);
+
+/* The owner's combine (src/runtime.c:2440-2466) for `rows` decode rows:
+ * part_*[r*ways + 0] is the owner's own finalist, part_*[r*ways + i] (i >= 1)
+ * the one rank part_ranks[r*ways + i] sent.  span_first/span_rows (host
+ * arrays of `ways` entries, by way) give each way's vocabulary rows, as
+ * fg_output_split_span does for the reference vocabulary; they must tile
+ * [0, vocab).  Ranks map to ways as fg_output_split_way_for_rank.  Per row:
+ * tokens[r] and logits_out[r] (may be NULL) get the combined finalist and
+ * row_status[r] FG_OK, or FG_ERR_MISMATCH (token 0xffffffff) when a rank owns
+ * no slice, an id is outside its rank's span, or the result is non-finite or
+ * >= vocab. */
+fg_status fg_hip_output_split_combine(uint32_t *tokens, float *logits_out, int32_t *row_status,
+                                      const float *part_values, const uint32_t *part_ids,
+                                      const uint8_t *part_ranks, uint32_t rows, uint32_t ways,
+                                      uint32_t vocab, const uint32_t *span_first,
+                                      const uint32_t *span_rows, void *stream, fg_error *err);
+
 #ifdef __cplusplus
 }
 #endif

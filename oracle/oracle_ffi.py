@@ -304,3 +304,52 @@ def topk_reduce_step(scores: np.ndarray, ids: np.ndarray):
         out_s[g * per:g * per + keep.size] = s[keep]
         out_i[g * per:g * per + keep.size] = i[keep]
     return out_s, out_i
+
+
+# ---- vocabulary-split greedy output ------------------------------------------
+
+SPLIT_RANKS = (4, 0, 1, 2)  # way -> rank, src/protocol.c:23-44
+STATUS_MISMATCH = 5
+
+
+def output_better(a: float, ai: int, b: float, bi: int) -> bool:
+    """fg_output_better (src/output.c:484-492): the same order as the top-512
+    reduction's comparator."""
+    return reduce_before(a, ai, b, bi)
+
+
+def slice_finalists(logits: np.ndarray, first_row: int):
+    """The reduction of fg_output_slice_run (src/output.c:341-363) per row of
+    logits[rows, slice]: the best (value, id) in fg_output_better's order,
+    ids first_row + i, status 5 (FG_ERR_MISMATCH) when the value is
+    non-finite."""
+    rows, n = logits.shape
+    ids = np.arange(first_row, first_row + n, dtype=np.uint32)
+    vals = np.empty(rows, dtype=np.float32)
+    out = np.empty(rows, dtype=np.uint32)
+    status = np.zeros(rows, dtype=np.int32)
+    for r in range(rows):
+        best = int(np.lexsort(reduce_order_key(logits[r], ids))[0])
+        vals[r], out[r] = logits[r, best], ids[best]
+        status[r] = 0 if np.isfinite(vals[r]) else STATUS_MISMATCH
+    return vals, out, status
+
+
+def split_combine_row(values, ids, ranks, ways: int, vocab: int, spans):
+    """The owner's combine (src/runtime.c:2440-2466) for one row: entry 0 is
+    the owner's finalist, entries 1.. come with their ranks; spans[w] =
+    (first, rows).  Returns (status, token, value); token 0xffffffff on
+    failure."""
+    value, tid = float(np.float32(values[0])), int(ids[0])
+    for i in range(1, ways):
+        rank, rid = int(ranks[i]), int(ids[i])
+        if rank not in SPLIT_RANKS[:ways]:
+            return STATUS_MISMATCH, 0xFFFFFFFF, None
+        first, n = spans[SPLIT_RANKS[:ways].index(rank)]
+        if not first <= rid < first + n:
+            return STATUS_MISMATCH, 0xFFFFFFFF, None
+        if output_better(np.float32(values[i]), rid, value, tid):
+            value, tid = float(np.float32(values[i])), rid
+    if tid >= vocab or not np.isfinite(value):
+        return STATUS_MISMATCH, 0xFFFFFFFF, value
+    return 0, tid, value

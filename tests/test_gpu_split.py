@@ -1,0 +1,195 @@
+"""GPU parity of the vocabulary-split greedy output: per-slice finalists
+(fg_hip_output_slice_reduce) against the oracle's restatement of
+src/output.c:341-363, the device combine (fg_hip_output_split_combine)
+against src/runtime.c:2440-2466 restated, and the two together against the
+whole-vocabulary argmax."""
+import numpy as np
+import pytest
+
+import fg_hip
+import oracle_ffi as O
+
+pytestmark = pytest.mark.gpu
+
+Q38 = 248320
+
+
+def _rows(rng, rows, n, specials=True):
+    x = (np.round(rng.normal(0, 3, (rows, n)) * 8) / 8).astype(np.float32)  # many ties
+    if specials:
+        for r in range(rows):
+            kind = r % 6
+            if kind == 1:
+                x[r, rng.integers(0, n, 2)] = np.nan
+            elif kind == 2:
+                x[r, rng.integers(0, n, 2)] = np.inf
+            elif kind == 3:
+                x[r, rng.integers(0, n)] = -np.inf
+                x[r, rng.integers(0, n, 3)] = 40.0  # tie at the maximum
+            elif kind == 4:
+                x[r] = -0.0
+                x[r, rng.integers(0, n, 5)] = 0.0
+            elif kind == 5:
+                x[r, -1] = 50.0  # winner in the last, partial chunk
+    return x
+
+
+def _slice_reduce(dev, sl, x, stride=None, batch=None):
+    import torch
+    rows = batch if batch is not None else x.shape[0]
+    t = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    if stride is not None:
+        padded = torch.full((x.shape[0], stride), 7.0, device=dev)
+        padded[:, :x.shape[1]] = t
+        t = padded
+    vals = torch.empty(rows, dtype=torch.float32, device=dev)
+    ids = torch.empty(rows, dtype=torch.int32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    sl.reduce(t, vals, ids, st, batch_rows=rows)
+    torch.cuda.synchronize()
+    return vals.cpu().numpy(), ids.cpu().numpy().view(np.uint32), st.cpu().numpy()
+
+
+def _check(got, want):
+    gv, gi, gs = got
+    wv, wi, ws = want
+    assert np.array_equal(gi, wi)
+    assert np.array_equal(gv.view(np.uint32), wv.view(np.uint32))
+    assert np.array_equal(gs, ws)
+
+
+@pytest.mark.parametrize("ways,way", [(2, 0), (2, 1), (4, 0), (4, 3)])
+def test_slice_finalists_reference_spans(dev, ways, way):
+    first, n = fg_hip.split_span(ways, way)
+    rng = np.random.default_rng(ways * 10 + way)
+    x = _rows(rng, 24, n)
+    sl = fg_hip.OutputSlice(Q38, ways, first, n, 64)
+    assert sl.ways() == ways
+    _check(_slice_reduce(dev, sl, x), O.slice_finalists(x, first))
+    # Second call, fewer rows: the workspace came back to zero.
+    y = _rows(rng, 5, n)
+    _check(_slice_reduce(dev, sl, y), O.slice_finalists(y, first))
+
+
+@pytest.mark.parametrize("n,first,stride", [(1, 0, None), (3, 17, None), (8191, 5, None),
+                                            (8192, 0, None), (8193, 100, None),
+                                            (37_984, 113_952, 38_000), (1001, 9, 1003)])
+def test_slice_finalists_shapes(dev, n, first, stride):
+    """Scalar path (unaligned stride or odd slice) and vector path, chunk edges."""
+    rng = np.random.default_rng(n)
+    x = _rows(rng, 12, n)
+    sl = fg_hip.OutputSlice(151_936, 4, first, n, 12)
+    _check(_slice_reduce(dev, sl, x, stride=stride), O.slice_finalists(x, first))
+
+
+def test_slice_arguments(dev):
+    with pytest.raises(fg_hip.FgStatusError) as e:
+        fg_hip.OutputSlice(Q38, 3, 0, 10, 4)
+    assert e.value.code == 2 and "invalid output slice arguments" in e.value.message
+    with pytest.raises(fg_hip.FgStatusError):
+        fg_hip.OutputSlice(Q38, 2, Q38 - 5, 6, 4)
+    with pytest.raises(fg_hip.FgStatusError):
+        fg_hip.OutputSlice(Q38, 2, 0, 10, 0)
+    import torch
+    sl = fg_hip.OutputSlice(Q38, 2, 0, 100, 4)
+    x = torch.zeros(5, 100, device=dev)
+    v = torch.empty(5, device=dev)
+    with pytest.raises(fg_hip.FgStatusError):  # more rows than max_batch_rows
+        sl.reduce(x, v, v, v, batch_rows=5)
+    with pytest.raises(fg_hip.FgStatusError):  # stride below the slice
+        sl.reduce(x, v, v, v, batch_rows=2, stride=50)
+
+
+def _combine(dev, vals, ids, ranks, ways, vocab, spans):
+    import torch
+    rows = vals.shape[0]
+    tv = torch.from_numpy(np.ascontiguousarray(vals, dtype=np.float32)).to(dev)
+    ti = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.uint32).view(np.int32)).to(dev)
+    tr = torch.from_numpy(np.ascontiguousarray(ranks, dtype=np.uint8)).to(dev)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    lg = torch.empty(rows, dtype=torch.float32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    fg_hip.split_combine(tok, lg, st, tv, ti, tr, rows, ways, vocab, spans)
+    torch.cuda.synchronize()
+    return tok.cpu().numpy().view(np.uint32), lg.cpu().numpy(), st.cpu().numpy()
+
+
+@pytest.mark.parametrize("ways", [2, 4])
+def test_split_end_to_end_matches_whole_vocab_argmax(dev, ways):
+    """Slices reduced on the device, finalists combined on the device: the
+    token and logit of the greedy argmax over the whole row."""
+    import torch
+    rng = np.random.default_rng(40 + ways)
+    rows = 32
+    x = _rows(rng, rows, Q38)
+    spans = [fg_hip.split_span(ways, w) for w in range(ways)]
+    vals = np.empty((rows, ways), dtype=np.float32)
+    ids = np.empty((rows, ways), dtype=np.uint32)
+    status = np.empty((rows, ways), dtype=np.int32)
+    tx = torch.from_numpy(x).to(dev)
+    for w, (first, n) in enumerate(spans):
+        sl = fg_hip.OutputSlice(Q38, ways, first, n, rows)
+        view = tx[:, first:first + n]
+        v = torch.empty(rows, device=dev)
+        i = torch.empty(rows, dtype=torch.int32, device=dev)
+        s = torch.empty(rows, dtype=torch.int32, device=dev)
+        sl.reduce(view, v, i, s, stride=Q38)
+        torch.cuda.synchronize()
+        vals[:, w], ids[:, w], status[:, w] = v.cpu().numpy(), u32(i), s.cpu().numpy()
+    ranks = np.tile(np.array([0] + [(4, 0, 1, 2)[w] for w in range(1, ways)], np.uint8), (rows, 1))
+    tok, lg, st = _combine(dev, vals, ids, ranks, ways, Q38, spans)
+    wv, wi, ws = O.slice_finalists(x, 0)
+    assert np.array_equal(tok[ws == 0], wi[ws == 0])
+    assert np.array_equal(lg[ws == 0].view(np.uint32), wv[ws == 0].view(np.uint32))
+    assert np.array_equal(st, ws)  # non-finite whole-row winners fail the combine
+    assert np.all(tok[ws != 0] == 0xFFFFFFFF)
+
+
+def u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def test_split_combine_matches_oracle_with_bad_partials(dev):
+    rng = np.random.default_rng(7)
+    ways, vocab, rows = 4, 151_936, 500
+    q = vocab // 4
+    spans = [(w * q, q) for w in range(4)]
+    vals = rng.normal(0, 1, (rows, ways)).astype(np.float32)
+    ids = np.empty((rows, ways), dtype=np.uint32)
+    ranks = np.zeros((rows, ways), dtype=np.uint8)
+    for r in range(rows):
+        order = rng.permutation(3) + 1  # remote ways in any order
+        ids[r, 0] = rng.integers(0, q)
+        for j, w in enumerate(order, start=1):
+            ranks[r, j] = (4, 0, 1, 2)[w]
+            ids[r, j] = w * q + rng.integers(0, q)
+        kind = r % 10
+        if kind == 1:
+            ranks[r, 2] = 3  # owns no slice
+        elif kind == 2:
+            ids[r, 1] = ids[r, 0]  # outside its rank's span
+        elif kind == 3:
+            vals[r, 3] = np.nan  # non-finite winner
+        elif kind == 4:
+            vals[r, :] = 1.5  # ties: lowest id
+        elif kind == 5:
+            vals[r, 0] = np.inf
+        elif kind == 6:
+            ids[r, 0] = 0xFFFFFFFF  # owner padding
+        elif kind == 7:
+            ids[r, 3] = vocab + 4  # beyond the vocabulary
+    tok, lg, st = _combine(dev, vals, ids, ranks, ways, vocab, spans)
+    for r in range(rows):
+        ws, wt, wv = O.split_combine_row(vals[r], ids[r], ranks[r], ways, vocab, spans)
+        assert st[r] == ws and tok[r] == wt, r
+        if ws == 0:
+            assert lg[r] == np.float32(wv)
+
+
+def test_split_combine_arguments(dev):
+    import torch
+    z = torch.zeros(8, dtype=torch.int32, device=dev)
+    with pytest.raises(fg_hip.FgStatusError):  # spans do not tile the vocabulary
+        fg_hip.split_combine(z, None, z, z, z, z, 2, 2, 100, [(0, 50), (50, 49)])
+    with pytest.raises(fg_hip.FgStatusError):
+        fg_hip.split_combine(z, None, z, z, z, z, 2, 3, 99, [(0, 33), (33, 33), (66, 33)])
