@@ -16,6 +16,11 @@ row reduced to one finalist (fg_hip_output_slice_reduce) and the finalists
 of all ways combined (fg_hip_output_split_combine); the other ways'
 finalists are reduced once, untimed, as the other ranks would send them.
 
+`--lm-head` times the producer of the logits instead: the reference's LM
+head (248,320 x 2,560 Q8_0 weights in the cooked layout, random bytes with
+binary16 scales in [1e-3, 2e-2]) times `--tokens` hidden vectors, fused with
+each token's greedy finalist (fg_hip_output_slice_run_dense, ways 1).
+
 `--config N` times the other configurations of BASELINE.json the same way
 (1: one greedy row; 3: 256 rows, whole-row nucleus; 4: 128 rows, quantised
 logits, greedy or sampled; 5: 1,024 rows with top-20 log-probs).  The driver
@@ -180,6 +185,73 @@ def cpu_baseline(x, c, u, gpu_tokens, budget_s):
     }, parity
 
 
+LM_VOCAB, LM_WIDTH = 248_320, 2_560
+
+
+def lm_head_bench(args, torch, fg_hip, dev):
+    tokens = args.tokens
+    tile = fg_hip.lib().fg_q8_0_cooked_tile_bytes(LM_WIDTH)
+    nbytes = fg_hip.lib().fg_q8_0_cooked_matrix_bytes(LM_WIDTH, LM_VOCAB)
+    tiles = nbytes // tile
+    g = torch.Generator(device=dev)
+    g.manual_seed(38)
+    w = torch.randint(0, 256, (tiles, tile), dtype=torch.uint8, device=dev, generator=g)
+    scales = 16 * (LM_WIDTH // 32)
+    d = (torch.rand((tiles, scales), device=dev, generator=g) * 0.019 + 0.001).to(torch.float16)
+    w[:, :2 * scales] = d.view(torch.uint8)
+    x = torch.randn((tokens, LM_WIDTH), device=dev, generator=g)
+    sl = fg_hip.OutputSlice(LM_VOCAB, 1, 0, LM_VOCAB, max(tokens, 1))
+    vals = torch.empty(tokens, device=dev)
+    ids = torch.empty(tokens, dtype=torch.int32, device=dev)
+    status = torch.empty(tokens, dtype=torch.int32, device=dev)
+    logits = torch.empty(tokens * LM_VOCAB, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        if args.unfused:
+            fg_hip.dense_q8_0_cooked(logits, w, x, LM_WIDTH, LM_VOCAB, tokens,
+                                     stream=stream.cuda_stream)
+        else:
+            sl.run_dense(w, x, LM_WIDTH, tokens, vals, ids, status, stream=stream.cuda_stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end)
+    per_s = ms / 1e3 / args.steps
+    if not args.unfused:
+        fg_hip.dense_q8_0_cooked(logits, w, x, LM_WIDTH, LM_VOCAB, tokens, stream=stream.cuda_stream)
+        y = logits.view(tokens, LM_VOCAB)
+        torch.cuda.synchronize()
+        assert bool((ids.to(torch.int64) == torch.argmax(y, dim=1)).all()), "finalist != argmax"
+        assert int(status.abs().sum()) == 0
+    alg = nbytes + 4 * LM_WIDTH * tokens + (4 * LM_VOCAB * tokens if args.unfused else 0)
+    kernel = "fg::dense_q8_cooked_kernel" if args.unfused else "fg::dense_q8_finalist_kernel"
+    print(json.dumps({
+        "metric": f"LM-head tokens/sec (Q8_0 {LM_VOCAB} x {LM_WIDTH}, "
+                  f"{'logits' if args.unfused else 'fused greedy finalist'})",
+        "value": round(tokens / per_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "q8_0 x f32",
+        "data": "synthetic (random Q8_0 bytes, binary16 scales in [1e-3, 2e-2], N(0,1) hidden)",
+        "config": {"workload": f"lm-head-{'plain' if args.unfused else 'finalist'}-t{tokens}",
+                   "rows": LM_VOCAB, "width": LM_WIDTH, "tokens": tokens,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(alg / per_s / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(alg / per_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": kernel, "algorithmic_bytes_per_launch": alg,
+                     "launch_us": round(per_s * 1e6, 3)},
+        "wall_s": round(wall, 3)}))
+
+
 def split_bench(args, torch, fg_hip, dev, w, sets, nsets, batch_bytes):
     ways, rows = args.split, w.rows
     quarter = VOCAB // ways
@@ -275,6 +347,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--split", type=int, default=0, choices=(0, 2, 4),
                     help="time the owner's side of the vocabulary-split greedy output")
+    ap.add_argument("--lm-head", action="store_true",
+                    help="time the Q8_0 LM-head product fused with the greedy finalist")
+    ap.add_argument("--tokens", type=int, default=1, help="--lm-head: hidden vectors per step")
+    ap.add_argument("--unfused", action="store_true",
+                    help="--lm-head: the plain product writing logits (no finalist)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 1 GiB device copy (the rocprof FETCH/WRITE_SIZE reference)")
     args = ap.parse_args()
@@ -300,6 +377,9 @@ def main():
         print(json.dumps({"calibration": "copy", "bytes_read": src.numel() * 4,
                           "bytes_written": dst.numel() * 4, "launches": args.steps}))
         return
+
+    if args.lm_head:
+        return lm_head_bench(args, torch, fg_hip, dev)
 
     w = Workload(args.config, fg_hip, sampled=not args.greedy)
     batch_bytes = 8 * VOCAB * w.rows

@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include "fg_sampler_hip.h"
+#include "fg_dense_kernels.hpp"
 #include "fg_nucleus_kernels.hpp"
 #include "fg_sample_kernels.hpp"
 #include "fg_split_kernels.hpp"
@@ -69,6 +70,52 @@ const SampleLaunch* const kVecLaunch =
 // Rows that are not 16-byte aligned: scalar loads, every part compiled in.
 const SampleLaunch kScalarLaunch =
     launch_sample<fg::Features<false, true, true, true, true, true>>;
+
+// ---- Q8_0 cooked matrix-vector launch shapes
+
+constexpr uint32_t kDensePassTokens = 2;  // tokens per pass over the weights
+
+bool dense_geometry(uint32_t in, uint32_t rows, fg::DenseArgs* a) {
+  if (!in || in % 32u || in * kDensePassTokens > fg::kDenseLdsFloats || !rows) return false;
+  const uint64_t blocks = in / 32u;
+  a->quant_offset = (fg::kCookRows * blocks * 2u + 63u) & ~63ull;
+  a->tile_bytes = (a->quant_offset + fg::kCookRows * blocks * 32u + 63u) & ~63ull;
+  a->in = in;
+  a->rows = rows;
+  return a->tile_bytes <= UINT32_MAX;
+}
+
+// One tile per wave: the dispatcher balances waves better than a fixed
+// tile stride (a persistent grid left a ragged last round).
+uint32_t dense_groups(uint32_t rows) {
+  const uint64_t tiles = (rows + fg::kCookRows - 1u) / fg::kCookRows;
+  return static_cast<uint32_t>((tiles + 3u) / 4u);
+}
+
+template <bool kFused>
+hipError_t dense_launch(fg::DenseArgs a, uint32_t tokens, hipStream_t stream) {
+  const uint32_t groups = dense_groups(a.rows);
+  for (uint32_t t0 = 0; t0 < tokens; t0 += kDensePassTokens) {
+    a.token0 = t0;
+    a.tokens = tokens - t0 < kDensePassTokens ? tokens - t0 : kDensePassTokens;
+    if (a.tokens == 1u) {
+      const size_t lds = sizeof(float) * a.in;
+      if (kFused)
+        fg::dense_q8_finalist_kernel<1><<<groups, fg::kDenseBlock, lds, stream>>>(a);
+      else
+        fg::dense_q8_cooked_kernel<1><<<groups, fg::kDenseBlock, lds, stream>>>(a);
+    } else {
+      const size_t lds = sizeof(float) * a.in * 2u;
+      if (kFused)
+        fg::dense_q8_finalist_kernel<2><<<groups, fg::kDenseBlock, lds, stream>>>(a);
+      else
+        fg::dense_q8_cooked_kernel<2><<<groups, fg::kDenseBlock, lds, stream>>>(a);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
 
 }  // namespace
 
@@ -174,7 +221,7 @@ fg_status fg_hip_output_slice_create(fg_hip_output_slice** out, uint32_t vocab, 
                                      uint32_t max_batch_rows, fg_error* err) {
   if (out) *out = nullptr;
   if (!out || !vocab || vocab == UINT32_MAX || !rows || first_row >= vocab ||
-      rows > vocab - first_row || (ways != 2u && ways != 4u) || !max_batch_rows ||
+      rows > vocab - first_row || (ways != 1u && ways != 2u && ways != 4u) || !max_batch_rows ||
       max_batch_rows > 65535u)
     return arg_fail(err, "invalid output slice arguments");
   fg_hip_output_slice* s = static_cast<fg_hip_output_slice*>(calloc(1, sizeof(*s)));
@@ -222,6 +269,48 @@ fg_status fg_hip_output_slice_reduce(fg_hip_output_slice* s, const float* logits
         s->d_arrivals);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "output slice launch");
+}
+
+// ---- Q8_0 cooked matrix-vector products ------------------------------------
+
+
+fg_status fg_hip_dense_q8_0_cooked(float* output, const void* weights, const float* input,
+                                   uint32_t in, uint32_t rows, uint32_t tokens, float scale,
+                                   void* stream, fg_error* err) {
+  fg::DenseArgs a{};
+  if (!output || !weights || !input || !tokens || !dense_geometry(in, rows, &a) ||
+      !aligned16(weights) || !aligned16(input))
+    return arg_fail(err, "invalid cooked Q8_0 dense dispatch");
+  a.w = static_cast<const uint8_t*>(weights);
+  a.x = input;
+  a.y = output;
+  a.scale = scale;
+  const hipError_t e = dense_launch<false>(a, tokens, as_stream(stream));
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "cooked Q8_0 dense launch");
+}
+
+fg_status fg_hip_output_slice_run_dense(fg_hip_output_slice* s, const void* weights,
+                                        const float* hidden, uint32_t in, uint32_t tokens,
+                                        float scale, float* values, uint32_t* ids,
+                                        int32_t* row_status, float* logits, void* stream,
+                                        fg_error* err) {
+  fg::DenseArgs a{};
+  if (!s || !weights || !hidden || !values || !ids || !row_status || !tokens ||
+      tokens > s->max_batch || s->first_row % fg::kCookRows || !dense_geometry(in, s->rows, &a) ||
+      !aligned16(weights) || !aligned16(hidden))
+    return arg_fail(err, "invalid output slice run arguments");
+  a.w = static_cast<const uint8_t*>(weights);
+  a.x = hidden;
+  a.y = logits;
+  a.scale = scale;
+  a.first_row = s->first_row;
+  a.keys = s->d_keys;
+  a.arrivals = s->d_arrivals;
+  a.values = values;
+  a.ids = ids;
+  a.status = row_status;
+  const hipError_t e = dense_launch<true>(a, tokens, as_stream(stream));
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "output slice dense launch");
 }
 
 fg_status fg_hip_output_split_combine(uint32_t* tokens, float* logits_out, int32_t* row_status,

@@ -1,6 +1,6 @@
 // Vocabulary-split greedy output on the device: each rank's slice of the
 // logits reduced to one (value, id) finalist per decode row, and the owner's
-// combine of the finalists (reference src/output.c:341-363, 484-497;
+// combine of the finalists (reference src/output.c:320-344, 484-497;
 // src/runtime.c:2440-2466).  The order is fg_output_better's, which is
 // greedy_comp's: padding last, non-finite first (lower id), then the larger
 // value, then the lower id.

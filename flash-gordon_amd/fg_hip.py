@@ -45,6 +45,9 @@ EXPORTS = (
     "fg_output_split_rank", "fg_output_split_span", "fg_output_split_combine_finalists",
     "fg_hip_output_slice_create", "fg_hip_output_slice_destroy", "fg_hip_output_slice_ways",
     "fg_hip_output_slice_reduce", "fg_hip_output_split_combine",
+    "fg_f16_to_f32", "fg_f32_to_f16", "fg_quantize_q8_0", "fg_dequantize_q8_0",
+    "fg_q8_0_cooked_tile_bytes", "fg_q8_0_cooked_matrix_bytes", "fg_cook_q8_0_rows",
+    "fg_uncook_q8_0_rows", "fg_hip_dense_q8_0_cooked", "fg_hip_output_slice_run_dense",
 )
 
 
@@ -141,6 +144,17 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_hip_output_slice_reduce": (C.c_int, [P, P, u64, u32, P, P, P, P, E]),
         "fg_hip_output_split_combine":
             (C.c_int, [P, P, P, P, P, P, u32, u32, u32, P, P, P, E]),
+        "fg_f16_to_f32": (f32, [C.c_uint16]),
+        "fg_f32_to_f16": (C.c_uint16, [f32]),
+        "fg_quantize_q8_0": (None, [P, P, u64]),
+        "fg_dequantize_q8_0": (None, [P, P, u64]),
+        "fg_q8_0_cooked_tile_bytes": (u64, [u32]),
+        "fg_q8_0_cooked_matrix_bytes": (u64, [u32, u32]),
+        "fg_cook_q8_0_rows": (C.c_bool, [P, P, u64, u32, u32]),
+        "fg_uncook_q8_0_rows": (C.c_bool, [P, P, u64, u32, u32]),
+        "fg_hip_dense_q8_0_cooked": (C.c_int, [P, P, P, u32, u32, u32, f32, P, E]),
+        "fg_hip_output_slice_run_dense":
+            (C.c_int, [P, P, P, u32, u32, f32, P, P, P, P, P, E]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -268,6 +282,35 @@ def history_decode(payload: bytes, capacity: int, vocab=None):
     return storage[:h.count].tolist(), h.session_slot
 
 
+# ---- Q8_0 weights (host) and products (device) -----------------------------
+
+def quantize_q8_0(x):
+    """fg_quantize_q8_0 over a float32 array (size a multiple of 32) -> bytes as uint8."""
+    import numpy as np
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.zeros(x.size // 32 * 34, dtype=np.uint8)
+    lib().fg_quantize_q8_0(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def cook_q8_0(packed, width, rows):
+    """fg_cook_q8_0_rows: packed Q8_0 rows -> cooked tiles (uint8 array)."""
+    import numpy as np
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    n = lib().fg_q8_0_cooked_matrix_bytes(width, rows)
+    out = np.empty(n, dtype=np.uint8)
+    if not n or not lib().fg_cook_q8_0_rows(packed.ctypes.data, out.ctypes.data, n, width, rows):
+        raise ValueError("fg_cook_q8_0_rows failed")
+    return out
+
+
+def dense_q8_0_cooked(out, weights, x, width, rows, tokens, scale=1.0, stream=None):
+    """fg_hip_dense_q8_0_cooked: out[t*rows + r] = scale * W[r] . x[t]."""
+    err = FgError()
+    _check(lib().fg_hip_dense_q8_0_cooked(_ptr(out), _ptr(weights), _ptr(x), width, rows, tokens,
+                                          scale, _stream(stream), C.byref(err)), err)
+
+
 # ---- vocabulary-split greedy output ----------------------------------------
 
 def split_span(ways: int, way: int) -> tuple[int, int]:
@@ -312,6 +355,15 @@ class OutputSlice:
 
     def ways(self) -> int:
         return self._lib.fg_hip_output_slice_ways(self.handle)
+
+    def run_dense(self, weights, hidden, width, tokens, values, ids, row_status, scale=1.0,
+                  logits=None, stream=None):
+        """fg_hip_output_slice_run_dense: the slice's cooked rows times hidden,
+        fused with each token's finalist."""
+        err = FgError()
+        _check(self._lib.fg_hip_output_slice_run_dense(
+            self.handle, _ptr(weights), _ptr(hidden), width, tokens, scale, _ptr(values),
+            _ptr(ids), _ptr(row_status), _ptr(logits), _stream(stream), C.byref(err)), err)
 
     def reduce(self, logits, values, ids, row_status, batch_rows=None, stride=None, stream=None):
         batch_rows = batch_rows if batch_rows is not None else logits.shape[0]

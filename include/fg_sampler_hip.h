@@ -187,6 +187,18 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip *sampler, uint32_t *co
                                            const int32_t *row_status, uint32_t rows,
                                            void *stream, fg_error *err);
 
+/* ---- Q8_0 matrix-vector products over cooked weights (fg_quant.h) ----
+ * output[t*rows + r] = scale * sum_i w(r, i) * input[t*in + i] for t <
+ * tokens, r < rows, w the cooked Q8_0 rows (ceil(rows/16) tiles of
+ * fg_q8_0_cooked_tile_bytes(in) bytes, 16-byte aligned; so is input).  Sums
+ * are f32 in the device's own order (within 1e-5 of the exact product's sum
+ * of magnitudes).  Errors: in == 0, in % 32, in > 8192, tokens == 0, rows
+ * == 0, null or unaligned pointers ("invalid cooked Q8_0 dense dispatch").
+ * Replaces fg_vk_dense_q8_0_f32 for cooked weights (src/vk.c:1451-1453). */
+fg_status fg_hip_dense_q8_0_cooked(float *output, const void *weights, const float *input,
+                                   uint32_t in, uint32_t rows, uint32_t tokens, float scale,
+                                   void *stream, fg_error *err);
+
 /* ---- vocabulary-split greedy output (fg_output_split.h has the layout) ----
  * A rank holding vocabulary rows [first_row, first_row + rows) of the LM head
  * reduces its logits to one (value, id) finalist per decode row; the output
@@ -195,18 +207,18 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip *sampler, uint32_t *co
 typedef struct fg_hip_output_slice fg_hip_output_slice;
 
 /* Mirrors fg_output_slice_create (src/output.c:234-258) without the model:
- * `vocab` is the full vocabulary, `ways` 2 or 4, the slice non-empty and
+ * `vocab` is the full vocabulary, `ways` 2 or 4 (or 1), the slice non-empty and
  * inside [0, vocab), and `max_batch_rows` (1..65535) the most decode rows
- * one call reduces.  FG_ERR_ARGUMENT ("invalid output slice arguments") otherwise;
+ * one call reduces.  `ways` 1 (an extension) is the whole head on one GPU.  FG_ERR_ARGUMENT ("invalid output slice arguments") otherwise;
  * FG_ERR_OOM when the workspace cannot be allocated. */
 fg_status fg_hip_output_slice_create(fg_hip_output_slice **out, uint32_t vocab, uint32_t ways,
                                      uint32_t first_row, uint32_t rows,
                                      uint32_t max_batch_rows, fg_error *err);
 void fg_hip_output_slice_destroy(fg_hip_output_slice *slice);
-/* ways of the slice, 0 for NULL (fg_output_slice_ways, src/output.c:336). */
+/* ways of the slice, 0 for NULL (fg_output_slice_ways, src/output.c:318). */
 uint32_t fg_hip_output_slice_ways(const fg_hip_output_slice *slice);
 
-/* The reduction half of fg_output_slice_run (src/output.c:341-363) for
+/* The reduction half of fg_output_slice_run (src/output.c:320-344) for
  * batch_rows decode rows: logits[r*stride + i], i < rows, is the logit of
  * vocabulary id first_row + i.  values[r], ids[r] receive the row's best
  * (value, id) in fg_output_better's order; row_status[r] is FG_OK, or
@@ -217,6 +229,19 @@ fg_status fg_hip_output_slice_reduce(fg_hip_output_slice *slice, const float *lo
                                      uint64_t stride, uint32_t batch_rows, float *values,
                                      uint32_t *ids, int32_t *row_status, void *stream,
                                      fg_error *err);
+
+/* fg_output_slice_run_hidden (src/output.c:367-383): its dense product
+ * (output_slice_reduce, src/output.c:320-344) fused with its reduction: weights are the slice's cooked rows
+ * (its first_row must be a multiple of 16), hidden[t*in ..] the inputs of
+ * tokens t < tokens (<= max_batch_rows).  values/ids/row_status as
+ * fg_hip_output_slice_reduce over the logits fg_hip_dense_q8_0_cooked would
+ * write, bit for bit; logits (may be NULL) receives those logits too.  Ways
+ * 1 (an extension: the whole head on one GPU) is allowed at create. */
+fg_status fg_hip_output_slice_run_dense(fg_hip_output_slice *slice, const void *weights,
+                                        const float *hidden, uint32_t in, uint32_t tokens,
+                                        float scale, float *values, uint32_t *ids,
+                                        int32_t *row_status, float *logits, void *stream,
+                                        fg_error *err);
 
 /* The owner's combine (src/runtime.c:2440-2466) for `rows` decode rows:
  * part_*[r*ways + 0] is the owner's own finalist, part_*[r*ways + i] (i >= 1)

@@ -319,7 +319,7 @@ def output_better(a: float, ai: int, b: float, bi: int) -> bool:
 
 
 def slice_finalists(logits: np.ndarray, first_row: int):
-    """The reduction of fg_output_slice_run (src/output.c:341-363) per row of
+    """The reduction of fg_output_slice_run (src/output.c:320-344) per row of
     logits[rows, slice]: the best (value, id) in fg_output_better's order,
     ids first_row + i, status 5 (FG_ERR_MISMATCH) when the value is
     non-finite."""
@@ -353,3 +353,45 @@ def split_combine_row(values, ids, ranks, ways: int, vocab: int, spans):
     if tid >= vocab or not np.isfinite(value):
         return STATUS_MISMATCH, 0xFFFFFFFF, value
     return 0, tid, value
+
+
+# ---- Q8_0 cooked matrix-vector product ---------------------------------------
+
+def q8_0_dequantize_rows(packed: np.ndarray, width: int, rows: int) -> np.ndarray:
+    """Packed Q8_0 rows -> f64 [rows, width]: d (binary16, widened exactly) * q
+    (src/quant.c:45-47; the product is exact in f64)."""
+    blocks = width // 32
+    b = np.asarray(packed, dtype=np.uint8).reshape(rows, blocks, 34)
+    d = b[:, :, :2].copy().view(np.float16)[..., 0].astype(np.float64)
+    q = b[:, :, 2:].view(np.int8).astype(np.float64)
+    return (d[:, :, None] * q).reshape(rows, width)
+
+
+def dense_q8_0_f64(packed: np.ndarray, x: np.ndarray, width: int, rows: int, scale: float):
+    """scale * W x in f64 (exact products, f64 sums) for x [tokens, width];
+    returns (y [tokens, rows], magnitude [tokens, rows] = scale * sum |w x|),
+    the second bounding the f32 rounding error of any summation order."""
+    w = q8_0_dequantize_rows(packed, width, rows)
+    xs = np.asarray(x, dtype=np.float64)
+    return (xs @ w.T) * scale, (np.abs(xs) @ np.abs(w).T) * abs(scale)
+
+
+def dense_q8_0_f32_reference_loop(packed: np.ndarray, x: np.ndarray, width: int, rows: int,
+                                  scale: float) -> np.ndarray:
+    """The reference test's CPU product (tests/test_fg_vk.c:393-404): one f32
+    fmaf chain per row over delta*q and x, times scale; small sizes only."""
+    blocks = width // 32
+    b = np.asarray(packed, dtype=np.uint8).reshape(rows, blocks, 34)
+    d = b[:, :, :2].copy().view(np.float16)[..., 0].astype(np.float32)
+    q = b[:, :, 2:].view(np.int8).astype(np.float32)
+    x = np.asarray(x, dtype=np.float32)
+    out = np.empty((x.shape[0], rows), dtype=np.float32)
+    for t in range(x.shape[0]):
+        for r in range(rows):
+            acc = np.float32(0.0)
+            for blk in range(blocks):
+                for i in range(32):
+                    wv = np.float32(d[r, blk] * q[r, blk, i])
+                    acc = np.float32(float(wv) * float(x[t, blk * 32 + i]) + float(acc))
+            out[t, r] = np.float32(acc * np.float32(scale))
+    return out

@@ -1,6 +1,6 @@
 """GPU parity of the vocabulary-split greedy output: per-slice finalists
 (fg_hip_output_slice_reduce) against the oracle's restatement of
-src/output.c:341-363, the device combine (fg_hip_output_split_combine)
+src/output.c:320-344, the device combine (fg_hip_output_split_combine)
 against src/runtime.c:2440-2466 restated, and the two together against the
 whole-vocabulary argmax."""
 import numpy as np
