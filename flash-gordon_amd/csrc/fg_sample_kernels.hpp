@@ -734,7 +734,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   __shared__ double s_nm[kWaves];
   __shared__ double s_nz[kWaves];
   __shared__ double s_ne[kWaves];
-  __shared__ int s_last;
   __shared__ uint32_t s_wg_key;
 
   // readfirstlane: the wave index is uniform across the wave, so the slice
@@ -848,100 +847,85 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   Mass wmass{-INFINITY, 0.0, 0.0};
   if (F::kNuc && nuc) wmass = wave_mass_combine(static_cast<double>(st.nm), st.nz, st.ne);
 
+  // ---- the workgroup's result: wave 0 combines the four waves from LDS ----
+  if (F::kTop) s_top[wave][lane] = mine;
+  if (lane == 0) {
+    s_greedy[wave] = gbest;
+    s_lm[wave] = wm;
+    s_lz[wave] = wz;
+    s_nm[wave] = wmass.m;
+    s_nz[wave] = wmass.z;
+    s_ne[wave] = wmass.e;
+  }
+  __syncthreads();
+  if (wave != 0) return;
   uint64_t fin = 0ull;
   uint64_t g = 0ull;
   double m = -INFINITY, z = 0.0;
   Mass zs{-INFINITY, 0.0, 0.0};
-  if (a.chunks == 1u) {
-    // The whole row is in this workgroup: merge from LDS.
-    if (F::kTop) s_top[wave][lane] = mine;
-    if (lane == 0) {
-      s_greedy[wave] = gbest;
-      s_lm[wave] = wm;
-      s_lz[wave] = wz;
-      s_nm[wave] = wmass.m;
-      s_nz[wave] = wmass.z;
-      s_ne[wave] = wmass.e;
-    }
-    __syncthreads();
-    if (wave != 0) return;
-    if (F::kTop && kk) {
-      fin = mine;
-      for (int w = 1; w < kWaves; w++) fin = wave_merge_desc(fin, s_top[w][lane]);
-    }
-    for (int w = 0; w < kWaves; w++) {
-      g = s_greedy[w] > g ? s_greedy[w] : g;
-      if (lse) lse_accumulate(m, z, s_lm[w], s_lz[w], t_eff);
-      if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
-    }
+  if (F::kTop && kk) {
+    // (0,1) and (2,3) side by side, then the two results.
+    uint64_t a0 = s_top[0][lane], a1 = s_top[2][lane];
+    wave_merge_desc2(a0, s_top[1][lane], a1, s_top[3][lane]);
+    fin = readlane64(a1, 0) > readlane64(a0, kk - 1u) ? wave_merge_desc(a0, a1) : a0;
+  }
+  for (int w = 0; w < kWaves; w++) {
+    g = s_greedy[w] > g ? s_greedy[w] : g;
+    if (lse) lse_accumulate(m, z, s_lm[w], s_lz[w], t_eff);
+    if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
+  }
+  if (a.chunks == 1u) {  // the whole row is in this workgroup
     finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow);
     return;
   }
 
-  // Publish this wave's partials with device-coherent stores.
-  const uint64_t slot = (static_cast<uint64_t>(row) * a.chunks + chunk) * kWaves + wave;
-  if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, mine);
+  // Publish the workgroup's partials with device-coherent stores.
+  const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
+  if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin);
   if (lane == 0) {
-    if (F::kGreedy && greedy) store_coherent(a.greedy + slot, gbest);
+    if (F::kGreedy && greedy) store_coherent(a.greedy + slot, g);
     if (lse) {
-      store_coherent_f64(a.lse + slot * 2, wm);
-      store_coherent_f64(a.lse + slot * 2 + 1, wz);
+      store_coherent_f64(a.lse + slot * 2, m);
+      store_coherent_f64(a.lse + slot * 2 + 1, z);
     }
     if (F::kNuc && nuc) {
-      store_coherent_f64(a.zsum + slot * 3, wmass.m);
-      store_coherent_f64(a.zsum + slot * 3 + 1, wmass.z);
-      store_coherent_f64(a.zsum + slot * 3 + 2, wmass.e);
+      store_coherent_f64(a.zsum + slot * 3, zs.m);
+      store_coherent_f64(a.zsum + slot * 3 + 1, zs.z);
+      store_coherent_f64(a.zsum + slot * 3 + 2, zs.e);
     }
   }
   wait_memory();
-  __syncthreads();
   FG_TRACE(a, 3);
-  if (threadIdx.x == 0)
-    s_last = atomicAdd(&a.row_done[row * kLineWords], 1u) == a.chunks - 1u;
-  __syncthreads();
+  uint32_t arrived = 0u;
+  if (lane == 0) arrived = atomicAdd(&a.row_done[row * kLineWords], 1u);
+  arrived = __builtin_amdgcn_readfirstlane(arrived);
   FG_TRACE(a, 4);
-  if (!s_last) return;
+  if (arrived != a.chunks - 1u) return;
 
-  // ---- last workgroup of the row: merge the row's sorted wave lists ----
-  const uint32_t lists = a.chunks * kWaves;
-  const uint64_t row_slot = static_cast<uint64_t>(row) * lists;
+  // ---- last workgroup of the row: merge the other workgroups' lists ----
+  const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
   if (F::kTop && kk) {
-    uint64_t acc = 0ull;
-    // Wave w merges lists w, w+4, ...; loads go out in groups of 8.
-    for (uint32_t l0 = wave; l0 < lists; l0 += 8u * kWaves) {
+    // Eight lists per round, loaded together and merged as a tree of
+    // side-by-side pairs; this workgroup's own list is already in `fin`.
+    for (uint32_t c0 = 0; c0 < a.chunks; c0 += 8u) {
       uint64_t x[8];
 #pragma unroll
       for (int t = 0; t < 8; t++) {
-        const uint32_t li = l0 + t * kWaves;
-        x[t] = (li < lists && lane < kk) ? load_coherent(a.cand + (row_slot + li) * kMaxK + lane)
-                                         : 0ull;
+        const uint32_t c = c0 + t;
+        x[t] = (c < a.chunks && c != chunk && lane < kk)
+                   ? load_coherent(a.cand + (row_slot + c) * kMaxK + lane)
+                   : 0ull;
       }
-#pragma unroll
-      for (int t = 0; t < 8; t++) {
-        // A list whose best entry cannot enter the running top-kk is skipped.
-        const uint64_t kth = readlane64(acc, kk - 1u);
-        if (readlane64(x[t], 0) > kth) acc = wave_merge_desc(acc, x[t]);
-      }
+      wave_merge_desc2(x[0], x[1], x[2], x[3]);
+      wave_merge_desc2(x[4], x[5], x[6], x[7]);
+      wave_merge_desc2(x[0], x[2], x[4], x[6]);
+      wave_merge_desc2(fin, x[0], x[4], 0ull);
+      if (readlane64(x[4], 0) > readlane64(fin, kk - 1u)) fin = wave_merge_desc(fin, x[4]);
     }
-    s_top[wave][lane] = acc;
-    __syncthreads();
     FG_TRACE(a, 5);
-    // Waves 0 and 1 merge pairs side by side, then wave 0 merges the two.
-    if (wave < 2) {
-      const uint64_t o = s_top[wave + 2][lane];
-      if (readlane64(o, 0) > readlane64(acc, kk - 1u)) acc = wave_merge_desc(acc, o);
-    }
-    __syncthreads();
-    if (wave == 1) s_top[1][lane] = acc;
-    __syncthreads();
-    if (wave == 0) {
-      const uint64_t o = s_top[1][lane];
-      fin = readlane64(o, 0) > readlane64(acc, kk - 1u) ? wave_merge_desc(acc, o) : acc;
-    }
   }
-  if (wave != 0) return;
   if (F::kGreedy && greedy) {
-    for (uint32_t i = lane; i < lists; i += kWave) {
+    for (uint32_t i = lane; i < a.chunks; i += kWave) {
       const uint64_t x = load_coherent(a.greedy + row_slot + i);
       g = x > g ? x : g;
     }
@@ -949,14 +933,14 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   }
   if (lse) {
     double lm = -INFINITY, lz = 0.0;
-    for (uint32_t i = lane; i < lists; i += kWave)
+    for (uint32_t i = lane; i < a.chunks; i += kWave)
       lse_accumulate(lm, lz, load_coherent_f64(a.lse + (row_slot + i) * 2),
                      load_coherent_f64(a.lse + (row_slot + i) * 2 + 1), t_eff);
     wave_lse_combine(lm, lz, t_eff, &m, &z);
   }
   if (F::kNuc && nuc) {
     Mass lm{-INFINITY, 0.0, 0.0};
-    for (uint32_t i = lane; i < lists; i += kWave)
+    for (uint32_t i = lane; i < a.chunks; i += kWave)
       mass_accumulate(lm, load_coherent_f64(a.zsum + (row_slot + i) * 3),
                       load_coherent_f64(a.zsum + (row_slot + i) * 3 + 1),
                       load_coherent_f64(a.zsum + (row_slot + i) * 3 + 2));
