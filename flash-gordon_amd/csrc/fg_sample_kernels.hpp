@@ -49,6 +49,8 @@ constexpr uint32_t kStepElems = kStepQuads * 4u;
 // LDS staging per wave: fewer than 64 left over plus one full step.
 constexpr uint32_t kCap = 64u + kStepElems;
 constexpr uint32_t kMaxK = 64;       // largest top-k / log-prob count
+constexpr uint32_t kSpecMinK = 32;   // top lists longer than this stage speculatively
+constexpr uint32_t kSpecMaxSteps = 8;  // ... over wave slices of at most this many steps
 constexpr uint32_t kMaxChunks = 64;  // workgroups per row
 constexpr uint32_t kLineWords = 32;  // u32 per 128-byte cache line (row counters)
 
@@ -78,6 +80,7 @@ struct SampleArgs {
   // workspace, indexed by wave slot = (row * chunks + chunk) * kWaves + wave
   uint64_t* cand;        // [slot][kMaxK] top-kk composites of the wave, descending, 0 = empty
   uint64_t* greedy;      // [slot] greedy composite
+  uint32_t* spec;        // [slot] the wave's speculative stream key (0 = none)
   double* lse;           // [slot][2] (max s, sum exp((s - max)/T))
   double* zsum;          // [slot][3] whole-row nucleus mass (max, sum, error bound)
   uint32_t* row_done;    // [rows * kLineWords] arrivals, one cache line per row,
@@ -267,12 +270,14 @@ __device__ __forceinline__ void top_stage(TopList& t, uint64_t comp) {
 }
 
 // Stream form: stages value v (element `id`, later in the stream than every
-// list member) when it passes the float filter.  The entry is staged raw
+// list member) when it passes the float filter f (fM, or a higher
+// speculative filter).  The entry is staged raw
 // (id << 32 | float bits, marked by kRawTag) and becomes a composite when it
 // is drained: the per-element cost stays a compare, a count and one store.
 // +Inf passes the filter and is dropped at the drain (its key is 0).
-__device__ __forceinline__ void top_stage_stream(TopList& t, bool valid, float v, uint32_t id) {
-  const bool pass = valid && v >= t.fM;
+__device__ __forceinline__ void top_stage_stream(TopList& t, bool valid, float v, uint32_t id,
+                                                 float f) {
+  const bool pass = valid && v >= f;
   const uint64_t m = ballot(pass);
   if (m == 0ull) return;
   FG_COUNT(1, static_cast<unsigned long long>(__popcll(m)));
@@ -494,7 +499,8 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
 
 // Which parts of the pass a launch needs (the union over its rows).  Each
 // combination is its own instantiation, so a launch carries only its code.
-template <bool kVec_, bool kPen_, bool kGreedy_, bool kTop_, bool kLse_, bool kNuc_>
+template <bool kVec_, bool kPen_, bool kGreedy_, bool kTop_, bool kLse_, bool kNuc_,
+          bool kSpec_>
 struct Features {
   static constexpr bool kVec = kVec_;      // 16-byte aligned rows: vector loads
   static constexpr bool kPen = kPen_;      // some row applies penalties
@@ -502,6 +508,7 @@ struct Features {
   static constexpr bool kTop = kTop_;      // some row keeps a top list
   static constexpr bool kLse = kLse_;      // log-probs requested
   static constexpr bool kNuc = kNuc_;      // some row is a whole-row nucleus (top_k 0)
+  static constexpr bool kSpec = kSpec_;    // some top list is longer than kSpecMinK
 };
 
 template <bool kVec>
@@ -546,6 +553,8 @@ struct WaveState {
   double nz;     // nucleus: per-lane sum of f32 terms exp(s - nm)
   double ne;     // nucleus: per-lane sum exp(s - nm) (nm - s), the error bound
   bool first;
+  uint32_t KS;   // speculative key: only elements with key >= KS are staged
+  float fS;      // its float form (elements v >= fS are staged)
 };
 
 // Greedy update for one element in stream order (ids rise along a lane).
@@ -579,7 +588,8 @@ __device__ __forceinline__ uint64_t greedy_lane_comp(const WaveState& st) {
 // at or past q_end are clamped duplicates and are masked out.
 template <class F>
 __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, bool pen,
-                                             bool greedy, bool lse, bool nuc, float log2e_over_t,
+                                             bool greedy, bool lse, bool nuc, bool spec,
+                                             float log2e_over_t,
                                              float* prow, const f4* x, const u4* y, uint32_t q0,
                                              uint32_t q_end) {
   const uint32_t lane = lane_id();
@@ -698,6 +708,21 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
       }
       if (T) top_raise(st.t, key_floor(T));
       top_share(st.t, T);
+      if (spec) {
+        // Speculation: stage only keys >= the m-th largest lane maximum of
+        // this step, m a few more than the row's top-kk is expected to hold
+        // here.  What it skips is checked when the row is merged: a wave
+        // whose key lies above the row's kk-th is scanned again then.
+        const uint32_t m = 7u;
+        uint32_t S = 0u;
+#pragma unroll
+        for (int b = 31; b >= 12; b--) {
+          const uint32_t c = S | (1u << b);
+          if (static_cast<uint32_t>(__popcll(ballot(lane_max_key >= c))) >= m) S = c;
+        }
+        st.KS = S;
+        st.fS = S >= 0x00800000u ? key_to_float(S) : -3.402823466e38f;
+      }
       st.first = false;
     }
     top_adopt(st.t);  // the workgroup's bound (the other waves' first steps too)
@@ -709,17 +734,99 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
 #pragma unroll
       for (int e = 0; e < 4; e++)
         if (ok[j] && v[j][e] < INFINITY) lane_max = fmaxf(lane_max, v[j][e]);
-    if (ballot(lane_max >= st.t.fM) != 0ull) {
+    const float f = F::kSpec ? fmaxf(st.t.fM, st.fS) : st.t.fM;
+    if (ballot(lane_max >= f) != 0ull) {
       FG_COUNT(2, 1ull);
 #pragma unroll
       for (int j = 0; j < kStepVec; j++) {
         const uint32_t q = q0 + j * kWave + lane;
 #pragma unroll
-        for (int e = 0; e < 4; e++) top_stage_stream(st.t, ok[j], v[j][e], q * 4u + e);
+        for (int e = 0; e < 4; e++) top_stage_stream(st.t, ok[j], v[j][e], q * 4u + e, f);
       }
       top_drain(st.t, false);
     }
   }
+}
+
+// ---- speculation check ------------------------------------------------------
+
+// Reads wave slice `i` of the row again and merges into `fin` (the row's list)
+// the elements the wave skipped under its speculative key ks that beat the
+// list's kk-th entry.  One wave; `buf` is its free staging LDS.
+__device__ inline uint64_t rescan_slice(const SampleArgs& a, const RowParams& p, bool pen,
+                                        const float* lrow, const uint32_t* crow, uint64_t fin,
+                                        uint32_t kk, uint32_t ks, uint32_t i, uint64_t* buf,
+                                        uint32_t* wg_key) {
+  const uint32_t lane = lane_id();
+  const uint32_t wbegin = min(i * a.wave_elems, a.vocab);
+  const uint32_t wend = min(wbegin + a.wave_elems, a.vocab);
+  const float fS = ks >= 0x00800000u ? key_to_float(ks) : -3.402823466e38f;
+  const uint64_t kth = readlane64(fin, kk - 1u);
+  // shared = all ones: this list never publishes a workgroup bound.
+  TopList t{fin, kth ? kth : kFiniteComp - 1ull, buf, 0u, kk, -3.402823466e38f, wg_key,
+            0xffffffffu};
+  constexpr uint32_t kPer = 16;
+  for (uint32_t i0 = wbegin; i0 < wend; i0 += kPer * kWave) {
+    float v[kPer];
+    uint32_t c[kPer];
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; j++) {
+      const uint32_t idx = i0 + j * kWave + lane;
+      const bool valid = idx < wend;
+      v[j] = valid ? lrow[idx] : 0.0f;
+      c[j] = valid && pen ? crow[idx] : 0u;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; j++) {
+      const uint32_t idx = i0 + j * kWave + lane;
+      const bool valid = idx < wend;
+      float x = v[j];
+      if (c[j] != 0u) x = penalise(x, c[j], p.presence, p.frequency, p.repetition);
+      // Exactly the elements the stream skipped for fS (x < fS); the others
+      // were staged then or cannot enter the list.
+      top_stage(t, valid && x < fS ? make_comp(float_key(x), idx) : 0ull);
+    }
+    // One drain call site (kept small: this path is rare); a round adds at
+    // most 16 * 64 entries, which fit beside fewer than 64 left over.
+    const bool last = i0 + kPer * kWave >= wend;
+    if (last || t.n >= static_cast<uint32_t>(kWave)) top_drain(t, last);
+  }
+  return t.top;
+}
+
+// Every element a speculating wave skipped has a key below its key KS, so it
+// cannot enter the row's top-kk when KS is at most the key of the list's
+// kk-th entry; each wave of the row for which that fails is read again.
+// ks_lds holds the keys when the row is one workgroup, else they are read
+// from the workspace.
+// The keys of waves 0..63 come in as ks0 (lane i: wave i), loaded early.
+__device__ __forceinline__ uint32_t spec_key(const SampleArgs& a, uint32_t row, uint32_t i,
+                                             const uint32_t* ks_lds) {
+  const uint32_t n = a.chunks * static_cast<uint32_t>(kWaves);
+  if (i >= n) return 0u;
+  return a.chunks == 1u ? ks_lds[i] : load_coherent(a.spec + static_cast<uint64_t>(row) * n + i);
+}
+
+__device__ inline uint64_t spec_check(const SampleArgs& a, const RowParams& p, uint32_t row,
+                                      bool pen, const float* lrow, const uint32_t* crow,
+                                      uint64_t fin, uint32_t kk, const uint32_t* ks_lds,
+                                      uint32_t ks0, uint64_t* buf, uint32_t* wg_key) {
+  const uint32_t lane = lane_id();
+  const uint32_t n = a.chunks * static_cast<uint32_t>(kWaves);
+  for (uint32_t b = 0; b < n; b += kWave) {
+    uint32_t ks = b == 0u ? ks0 : spec_key(a, row, b + lane, ks_lds);
+    for (;;) {
+      const uint32_t kkey = comp_key(readlane64(fin, kk - 1u));
+      const uint64_t need = ballot(ks > kkey);
+      if (need == 0ull) break;
+      const uint32_t l = static_cast<uint32_t>(__builtin_ctzll(need));
+      const uint32_t w_ks = readlane32(ks, l);
+      FG_COUNT(4, 1ull);
+      fin = rescan_slice(a, p, pen, lrow, crow, fin, kk, w_ks, b + l, buf, wg_key);
+      if (lane == l) ks = 0u;
+    }
+  }
+  return fin;
 }
 
 // ---- the fused kernel ------------------------------------------------------
@@ -729,6 +836,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   __shared__ uint64_t s_buf[F::kTop ? kWaves : 1][F::kTop ? kCap : 1];
   __shared__ uint64_t s_top[kWaves][kWave];
   __shared__ uint64_t s_greedy[kWaves];
+  __shared__ uint32_t s_ks[kWaves];
   __shared__ double s_lm[kWaves];
   __shared__ double s_lz[kWaves];
   __shared__ double s_nm[kWaves];
@@ -752,6 +860,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const bool nuc = F::kNuc && !greedy && p.top_k == 0u;
   const uint32_t kk = greedy ? L : nuc ? kMaxK : (p.top_k > L ? p.top_k : L);
   const bool pen = (p.flags & kRowPenalties) && a.counts != nullptr;
+  // Speculative staging pays for top lists longer than kSpecMinK over short
+  // wave slices (measured: top-k 64 on 64 rows runs 16% faster); over long
+  // slices the exact filter soon passes it, and a check that fails would
+  // read a long slice again.
+  const bool spec = F::kSpec && !greedy && !nuc && kk > kSpecMinK &&
+                    a.wave_elems <= kSpecMaxSteps * kStepElems;
   const float t_eff = p.temperature > 0.0f ? p.temperature : 1.0f;
   const float log2e_over_t = 1.4426950408889634f / t_eff;
 
@@ -770,7 +884,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   }
   WaveState st{{0ull, kFiniteComp - 1ull, F::kTop ? s_buf[wave] : nullptr, 0u, F::kTop ? kk : 0u,
                 -3.402823466e38f, &s_wg_key, 0u},
-               -INFINITY, kInvalidId, kInvalidId, -INFINITY, 0.0f, -INFINITY, 0.0, 0.0, true};
+               -INFINITY, kInvalidId, kInvalidId, -INFINITY, 0.0f, -INFINITY, 0.0, 0.0, true,
+               0u, -3.402823466e38f};
   FG_TRACE(a, 0);
 
   if (q_end > q_begin) {
@@ -796,10 +911,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     load(xa, ya, q_begin);
     for (uint32_t q0 = q_begin;;) {
       load(xb, yb, q0 + kStepQuads);
-      process_step<F>(st, p, pen, greedy, lse, nuc, log2e_over_t, prow, xa, ya, q0, q_end);
+      process_step<F>(st, p, pen, greedy, lse, nuc, spec, log2e_over_t, prow, xa, ya, q0, q_end);
       if ((q0 += kStepQuads) >= q_end) break;
       load(xa, ya, q0 + kStepQuads);
-      process_step<F>(st, p, pen, greedy, lse, nuc, log2e_over_t, prow, xb, yb, q0, q_end);
+      process_step<F>(st, p, pen, greedy, lse, nuc, spec, log2e_over_t, prow, xb, yb, q0, q_end);
       if ((q0 += kStepQuads) >= q_end) break;
     }
   }
@@ -831,7 +946,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
           st.nz = ms.z;
           st.ne = ms.e;
         }
-        if (F::kTop && kk) top_stage(st.t, make_comp(valid ? float_key(v) : 0u, i0 + e));
+        // Below the speculative filter an element is left to the check.
+        if (F::kTop && kk)
+          top_stage(st.t, make_comp(valid && !(F::kSpec && v < st.fS) ? float_key(v) : 0u, i0 + e));
       }
     }
   }
@@ -851,6 +968,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   if (F::kTop) s_top[wave][lane] = mine;
   if (lane == 0) {
     s_greedy[wave] = gbest;
+    if (F::kSpec) s_ks[wave] = st.KS;
     s_lm[wave] = wm;
     s_lz[wave] = wz;
     s_nm[wave] = wmass.m;
@@ -874,81 +992,91 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (lse) lse_accumulate(m, z, s_lm[w], s_lz[w], t_eff);
     if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
   }
+  uint32_t ks0 = 0u;
   if (a.chunks == 1u) {  // the whole row is in this workgroup
-    finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow);
-    return;
-  }
+    if (spec) ks0 = spec_key(a, row, lane, s_ks);
+  } else {
+    // Publish the workgroup's partials with device-coherent stores.
+    const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
+    if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin);
+    if (spec && lane < static_cast<uint32_t>(kWaves))
+      store_coherent(a.spec + slot * kWaves + lane, s_ks[lane]);
+    if (lane == 0) {
+      if (F::kGreedy && greedy) store_coherent(a.greedy + slot, g);
+      if (lse) {
+        store_coherent_f64(a.lse + slot * 2, m);
+        store_coherent_f64(a.lse + slot * 2 + 1, z);
+      }
+      if (F::kNuc && nuc) {
+        store_coherent_f64(a.zsum + slot * 3, zs.m);
+        store_coherent_f64(a.zsum + slot * 3 + 1, zs.z);
+        store_coherent_f64(a.zsum + slot * 3 + 2, zs.e);
+      }
+    }
+    wait_memory();
+    FG_TRACE(a, 3);
+    uint32_t arrived = 0u;
+    if (lane == 0) arrived = atomicAdd(&a.row_done[row * kLineWords], 1u);
+    arrived = __builtin_amdgcn_readfirstlane(arrived);
+    FG_TRACE(a, 4);
+    if (arrived != a.chunks - 1u) return;
 
-  // Publish the workgroup's partials with device-coherent stores.
-  const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
-  if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin);
-  if (lane == 0) {
-    if (F::kGreedy && greedy) store_coherent(a.greedy + slot, g);
+    // ---- last workgroup of the row: merge the other workgroups' lists ----
+    const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
+    if (F::kTop && kk) {
+      // Eight lists per round, loaded together and merged as a tree of
+      // side-by-side pairs; this workgroup's own list is already in `fin`.
+      for (uint32_t c0 = 0; c0 < a.chunks; c0 += 8u) {
+        uint64_t x[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const uint32_t c = c0 + t;
+          x[t] = (c < a.chunks && c != chunk && lane < kk)
+                     ? load_coherent(a.cand + (row_slot + c) * kMaxK + lane)
+                     : 0ull;
+        }
+        if (spec && c0 == 0u) {
+          // The waves' speculative keys travel with the first lists (the
+          // asm keeps the load here instead of after the merges).
+          ks0 = spec_key(a, row, lane, s_ks);
+          asm volatile("" ::"v"(ks0));
+        }
+        wave_merge_desc2(x[0], x[1], x[2], x[3]);
+        wave_merge_desc2(x[4], x[5], x[6], x[7]);
+        wave_merge_desc2(x[0], x[2], x[4], x[6]);
+        wave_merge_desc2(fin, x[0], x[4], 0ull);
+        if (readlane64(x[4], 0) > readlane64(fin, kk - 1u)) fin = wave_merge_desc(fin, x[4]);
+      }
+      FG_TRACE(a, 5);
+    }
+    if (F::kGreedy && greedy) {
+      for (uint32_t i = lane; i < a.chunks; i += kWave) {
+        const uint64_t x = load_coherent(a.greedy + row_slot + i);
+        g = x > g ? x : g;
+      }
+      g = wave_max_u64(g);
+    }
     if (lse) {
-      store_coherent_f64(a.lse + slot * 2, m);
-      store_coherent_f64(a.lse + slot * 2 + 1, z);
+      double lm = -INFINITY, lz = 0.0;
+      for (uint32_t i = lane; i < a.chunks; i += kWave)
+        lse_accumulate(lm, lz, load_coherent_f64(a.lse + (row_slot + i) * 2),
+                       load_coherent_f64(a.lse + (row_slot + i) * 2 + 1), t_eff);
+      wave_lse_combine(lm, lz, t_eff, &m, &z);
     }
     if (F::kNuc && nuc) {
-      store_coherent_f64(a.zsum + slot * 3, zs.m);
-      store_coherent_f64(a.zsum + slot * 3 + 1, zs.z);
-      store_coherent_f64(a.zsum + slot * 3 + 2, zs.e);
+      Mass lm{-INFINITY, 0.0, 0.0};
+      for (uint32_t i = lane; i < a.chunks; i += kWave)
+        mass_accumulate(lm, load_coherent_f64(a.zsum + (row_slot + i) * 3),
+                        load_coherent_f64(a.zsum + (row_slot + i) * 3 + 1),
+                        load_coherent_f64(a.zsum + (row_slot + i) * 3 + 2));
+      zs = wave_mass_combine(lm.m, lm.z, lm.e);
     }
   }
-  wait_memory();
-  FG_TRACE(a, 3);
-  uint32_t arrived = 0u;
-  if (lane == 0) arrived = atomicAdd(&a.row_done[row * kLineWords], 1u);
-  arrived = __builtin_amdgcn_readfirstlane(arrived);
-  FG_TRACE(a, 4);
-  if (arrived != a.chunks - 1u) return;
-
-  // ---- last workgroup of the row: merge the other workgroups' lists ----
-  const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
-  if (F::kTop && kk) {
-    // Eight lists per round, loaded together and merged as a tree of
-    // side-by-side pairs; this workgroup's own list is already in `fin`.
-    for (uint32_t c0 = 0; c0 < a.chunks; c0 += 8u) {
-      uint64_t x[8];
-#pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const uint32_t c = c0 + t;
-        x[t] = (c < a.chunks && c != chunk && lane < kk)
-                   ? load_coherent(a.cand + (row_slot + c) * kMaxK + lane)
-                   : 0ull;
-      }
-      wave_merge_desc2(x[0], x[1], x[2], x[3]);
-      wave_merge_desc2(x[4], x[5], x[6], x[7]);
-      wave_merge_desc2(x[0], x[2], x[4], x[6]);
-      wave_merge_desc2(fin, x[0], x[4], 0ull);
-      if (readlane64(x[4], 0) > readlane64(fin, kk - 1u)) fin = wave_merge_desc(fin, x[4]);
-    }
-    FG_TRACE(a, 5);
-  }
-  if (F::kGreedy && greedy) {
-    for (uint32_t i = lane; i < a.chunks; i += kWave) {
-      const uint64_t x = load_coherent(a.greedy + row_slot + i);
-      g = x > g ? x : g;
-    }
-    g = wave_max_u64(g);
-  }
-  if (lse) {
-    double lm = -INFINITY, lz = 0.0;
-    for (uint32_t i = lane; i < a.chunks; i += kWave)
-      lse_accumulate(lm, lz, load_coherent_f64(a.lse + (row_slot + i) * 2),
-                     load_coherent_f64(a.lse + (row_slot + i) * 2 + 1), t_eff);
-    wave_lse_combine(lm, lz, t_eff, &m, &z);
-  }
-  if (F::kNuc && nuc) {
-    Mass lm{-INFINITY, 0.0, 0.0};
-    for (uint32_t i = lane; i < a.chunks; i += kWave)
-      mass_accumulate(lm, load_coherent_f64(a.zsum + (row_slot + i) * 3),
-                      load_coherent_f64(a.zsum + (row_slot + i) * 3 + 1),
-                      load_coherent_f64(a.zsum + (row_slot + i) * 3 + 2));
-    zs = wave_mass_combine(lm.m, lm.z, lm.e);
-  }
+  // One copy of the check and of the finish serves both paths.
+  if (spec) fin = spec_check(a, p, row, pen, lrow, crow, fin, kk, s_ks, ks0, s_buf[0], &s_wg_key);
   FG_TRACE(a, 6);
   finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow);
-  if (lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
+  if (a.chunks != 1u && lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
   FG_TRACE(a, 7);
 }
 

@@ -54,8 +54,10 @@ void launch_sample(uint32_t grid, hipStream_t s, const fg::SampleArgs& a) {
 
 template <int kBits>
 constexpr SampleLaunch vec_launch() {
+  // The speculative-staging bit only exists alongside top lists.
   return launch_sample<fg::Features<true, (kBits & 1) != 0, (kBits & 2) != 0, (kBits & 4) != 0,
-                                    (kBits & 8) != 0, (kBits & 16) != 0>>;
+                                    (kBits & 8) != 0, (kBits & 16) != 0,
+                                    (kBits & 4) != 0 && (kBits & 32) != 0>>;
 }
 
 template <int... kBits>
@@ -63,13 +65,16 @@ struct LaunchTable {
   static constexpr SampleLaunch table[sizeof...(kBits)] = {vec_launch<kBits>()...};
 };
 
-// Indexed by pen | greedy << 1 | top << 2 | lse << 3 | nucleus << 4.
+// Indexed by pen | greedy << 1 | top << 2 | lse << 3 | nucleus << 4 |
+// speculative << 5.
 const SampleLaunch* const kVecLaunch =
     LaunchTable<0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21,
-                22, 23, 24, 25, 26, 27, 28, 29, 30, 31>::table;
+                22, 23, 24, 25, 26, 27, 28, 29, 30, 31, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41,
+                42, 43, 44, 45, 46, 47, 48, 49, 50, 51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61,
+                62, 63>::table;
 // Rows that are not 16-byte aligned: scalar loads, every part compiled in.
 const SampleLaunch kScalarLaunch =
-    launch_sample<fg::Features<false, true, true, true, true, true>>;
+    launch_sample<fg::Features<false, true, true, true, true, true, true>>;
 
 // ---- Q8_0 cooked matrix-vector launch shapes
 
@@ -129,6 +134,7 @@ struct fg_sampler_hip {
   uint64_t slots;           // wave slots in the workspace
   uint64_t* d_cand;         // [slots][kMaxK]
   uint64_t* d_greedy;       // [slots]
+  uint32_t* d_spec;         // [slots] speculative stream keys
   double* d_lse;            // [slots][2]
   double* d_zsum;           // [slots][3]
   uint32_t* d_row_done;     // [max_rows * kLineWords]
@@ -420,6 +426,7 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMalloc(&s->d_params, sizeof(RowParams) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&s->d_cand, sizeof(uint64_t) * slots * fg::kMaxK);
   if (e == hipSuccess) e = hipMalloc(&s->d_greedy, sizeof(uint64_t) * slots);
+  if (e == hipSuccess) e = hipMalloc(&s->d_spec, sizeof(uint32_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->d_lse, sizeof(double) * slots * 2);
   if (e == hipSuccess) e = hipMalloc(&s->d_zsum, sizeof(double) * slots * 3);
   const size_t done_bytes = sizeof(uint32_t) * fg::kLineWords * max_rows;
@@ -450,6 +457,7 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   (void)hipFree(s->d_params);
   (void)hipFree(s->d_cand);
   (void)hipFree(s->d_greedy);
+  (void)hipFree(s->d_spec);
   (void)hipFree(s->d_lse);
   (void)hipFree(s->d_zsum);
   (void)hipFree(s->d_row_done);
@@ -535,6 +543,7 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
   a.lp_ids = b->logprob_ids;
   a.cand = s->d_cand;
   a.greedy = s->d_greedy;
+  a.spec = s->d_spec;
   a.lse = s->d_lse;
   a.zsum = s->d_zsum;
   a.row_done = s->d_row_done;
@@ -547,16 +556,19 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
                    wave_elems < (1u << 28) &&
                    (!b->counts || (aligned16(b->counts) && (b->counts_stride % 4u) == 0u));
   bool any_pen = false, any_greedy = false, any_top = b->logprobs != 0u, any_nuc = false;
+  bool any_spec = false;
   for (uint32_t r = 0; r < b->rows; r++) {
     const RowParams& rp = s->h_params[r];
     any_pen |= (rp.flags & fg::kRowPenalties) != 0u;
     any_greedy |= rp.temperature == 0.0f;
     any_top |= rp.temperature > 0.0f;
     any_nuc |= rp.temperature > 0.0f && rp.top_k == 0u;
+    any_spec |= rp.temperature > 0.0f && rp.top_k != 0u &&
+                (rp.top_k > b->logprobs ? rp.top_k : b->logprobs) > fg::kSpecMinK;
   }
   any_pen = any_pen && b->counts != nullptr;
   const int bits = (any_pen ? 1 : 0) | (any_greedy ? 2 : 0) | (any_top ? 4 : 0) |
-                   (b->logprobs ? 8 : 0) | (any_nuc ? 16 : 0);
+                   (b->logprobs ? 8 : 0) | (any_nuc ? 16 : 0) | (any_spec ? 32 : 0);
   const uint32_t grid = b->rows * chunks;
   (vec ? kVecLaunch[bits] : kScalarLaunch)(grid, as_stream(stream), a);
   // Whole-row nucleus rows whose cut lies past the kMaxK best are finished

@@ -327,3 +327,36 @@ def test_nucleus_mixed_with_top_k_rows_and_logprobs(dev):
     ref = W.oracle_run(w)
     assert ref["cutoff"][2] > 64
     check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), ref, "nucleus mixed", NUC_BOUNDARY)
+
+
+@pytest.mark.parametrize("k,logprobs", [(20, 0), (64, 0), (20, 40), (40, 0), (5, 0)])
+def test_speculative_filter_rescans(dev, k, logprobs):
+    """Rows built so that a wave's early elements hold most of the row's best
+    values: the speculative stream filter then skips elements that belong in
+    the row's top-k, and the merge must read those slices again.  Also
+    ascending, descending and tied rows, a row with few finite values, and
+    values just below the speculative filter.  Exact against the oracle."""
+    rng = np.random.default_rng(17 + k)
+    rows, vocab = 12, W.V
+    logits = rng.normal(0, 1, (rows, vocab)).astype(np.float32)
+    logits[0, :600] = 50 + rng.normal(0, 1, 600)                 # top values at the row start
+    logits[1] = np.linspace(-5, 5, vocab, dtype=np.float32)       # ascending
+    logits[2] = np.linspace(5, -5, vocab, dtype=np.float32)       # descending
+    logits[3, :] = 1.0                                            # all tied
+    logits[3, 5000:5100] = 2.0
+    logits[4, :] = -np.inf                                        # few finite values
+    logits[4, rng.choice(vocab, 90, replace=False)] = rng.normal(0, 1, 90)
+    logits[5, 37984:37984 + 1500] = 20 + rng.normal(0, 1, 1500)   # one slice holds the top
+    logits[6, 0:300:3] = 30.0                                     # tied top values, spread out
+    logits[7, 151_000:] = 40 + rng.normal(0, 1, vocab - 151_000)  # top values in the row tail
+    for r in (8, 9):                                              # clustered per 1024-element step
+        for b in range(0, vocab, 4096):
+            logits[r, b:b + 8] = 10 + rng.normal(0, 0.1, 8)
+    logits[10, :64 * 16] = 9.0 + np.arange(1024, dtype=np.float32) * 1e-3  # one value per lane
+    counts = np.zeros((rows, vocab), dtype=np.uint32)
+    counts[11, :300] = rng.integers(1, 5, 300)                    # penalties on the top values
+    logits[11, :300] = 60.0
+    configs = [W.cfg(0.8, 0.9, k, presence=0.4 if r == 11 else 0.0) for r in range(rows)]
+    w = dict(logits=logits, counts=counts, configs=configs,
+             uniforms=rng.random(rows).astype(np.float32), logprobs=logprobs)
+    check(w, run_hip(w, dev), W.oracle_run(w), f"speculation k={k} L={logprobs}")
