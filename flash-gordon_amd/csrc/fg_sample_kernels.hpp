@@ -50,7 +50,7 @@ constexpr uint32_t kStepElems = kStepQuads * 4u;
 constexpr uint32_t kCap = 64u + kStepElems;
 constexpr uint32_t kMaxK = 64;       // largest top-k / log-prob count
 constexpr uint32_t kSpecMinK = 32;   // top lists longer than this stage speculatively
-constexpr uint32_t kSpecMaxSteps = 8;  // ... over wave slices of at most this many steps
+constexpr uint32_t kSpecMaxSteps = 16;  // ... over wave slices of at most this many steps
 constexpr uint32_t kMaxChunks = 64;  // workgroups per row
 constexpr uint32_t kLineWords = 32;  // u32 per 128-byte cache line (row counters)
 
