@@ -50,7 +50,7 @@ constexpr uint32_t kStepElems = kStepQuads * 4u;
 constexpr uint32_t kCap = 64u + kStepElems;
 constexpr uint32_t kMaxK = 64;       // largest top-k / log-prob count
 constexpr uint32_t kSpecMinK = 32;   // top lists longer than this stage speculatively
-constexpr uint32_t kSpecMaxSteps = 16;  // ... over wave slices of at most this many steps
+constexpr uint32_t kSpecMaxSteps = 24;  // ... over wave slices of at most this many steps
 constexpr uint32_t kMaxChunks = 64;  // workgroups per row
 constexpr uint32_t kLineWords = 32;  // u32 per 128-byte cache line (row counters)
 
@@ -860,11 +860,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const bool nuc = F::kNuc && !greedy && p.top_k == 0u;
   const uint32_t kk = greedy ? L : nuc ? kMaxK : (p.top_k > L ? p.top_k : L);
   const bool pen = (p.flags & kRowPenalties) && a.counts != nullptr;
-  // Speculative staging pays for top lists longer than kSpecMinK over short
-  // wave slices (measured: top-k 64 on 64 rows runs 16% faster); over long
+  // Speculative staging pays for top lists longer than kSpecMinK (top-k
+  // rows and the whole-row nucleus's 64 best) over short wave slices
+  // (measured: top-k 64 on 64 rows 16% faster, config 3 6%); over long
   // slices the exact filter soon passes it, and a check that fails would
   // read a long slice again.
-  const bool spec = F::kSpec && !greedy && !nuc && kk > kSpecMinK &&
+  const bool spec = F::kSpec && !greedy && kk > kSpecMinK &&
                     a.wave_elems <= kSpecMaxSteps * kStepElems;
   const float t_eff = p.temperature > 0.0f ? p.temperature : 1.0f;
   const float log2e_over_t = 1.4426950408889634f / t_eff;

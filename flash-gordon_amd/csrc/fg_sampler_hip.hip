@@ -563,8 +563,9 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
     any_greedy |= rp.temperature == 0.0f;
     any_top |= rp.temperature > 0.0f;
     any_nuc |= rp.temperature > 0.0f && rp.top_k == 0u;
-    any_spec |= rp.temperature > 0.0f && rp.top_k != 0u &&
-                (rp.top_k > b->logprobs ? rp.top_k : b->logprobs) > fg::kSpecMinK;
+    any_spec |= rp.temperature > 0.0f &&
+                (rp.top_k == 0u ? fg::kMaxK : (rp.top_k > b->logprobs ? rp.top_k : b->logprobs)) >
+                    fg::kSpecMinK;
   }
   any_pen = any_pen && b->counts != nullptr;
   const int bits = (any_pen ? 1 : 0) | (any_greedy ? 2 : 0) | (any_top ? 4 : 0) |

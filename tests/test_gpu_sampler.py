@@ -329,11 +329,12 @@ def test_nucleus_mixed_with_top_k_rows_and_logprobs(dev):
     check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), ref, "nucleus mixed", NUC_BOUNDARY)
 
 
-@pytest.mark.parametrize("k,logprobs", [(20, 0), (64, 0), (20, 40), (40, 0), (5, 0)])
+@pytest.mark.parametrize("k,logprobs", [(20, 0), (64, 0), (20, 40), (40, 0), (5, 0), (0, 0)])
 def test_speculative_filter_rescans(dev, k, logprobs):
     """Rows built so that a wave's early elements hold most of the row's best
     values: the speculative stream filter then skips elements that belong in
-    the row's top-k, and the merge must read those slices again.  Also
+    the row's top-k (or a nucleus row's 64 best), and the merge must read
+    those slices again.  Also
     ascending, descending and tied rows, a row with few finite values, and
     values just below the speculative filter.  Exact against the oracle."""
     rng = np.random.default_rng(17 + k)
@@ -356,7 +357,13 @@ def test_speculative_filter_rescans(dev, k, logprobs):
     counts = np.zeros((rows, vocab), dtype=np.uint32)
     counts[11, :300] = rng.integers(1, 5, 300)                    # penalties on the top values
     logits[11, :300] = 60.0
-    configs = [W.cfg(0.8, 0.9, k, presence=0.4 if r == 11 else 0.0) for r in range(rows)]
+    # k == 0: the whole-row nucleus, whose list of the 64 best speculates too.
+    configs = [W.cfg(0.8, 0.9 if k else 0.2, k, presence=0.4 if r == 11 else 0.0)
+               for r in range(rows)]
     w = dict(logits=logits, counts=counts, configs=configs,
              uniforms=rng.random(rows).astype(np.float32), logprobs=logprobs)
-    check(w, run_hip(w, dev), W.oracle_run(w), f"speculation k={k} L={logprobs}")
+    if k:
+        check(w, run_hip(w, dev), W.oracle_run(w), f"speculation k={k} L={logprobs}")
+    else:
+        check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), W.oracle_run(w),
+              "speculation nucleus", NUC_BOUNDARY)
