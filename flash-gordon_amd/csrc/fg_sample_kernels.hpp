@@ -52,6 +52,8 @@ constexpr uint32_t kMaxK = 64;       // largest top-k / log-prob count
 constexpr uint32_t kSpecMinK = 32;   // top lists longer than this stage speculatively
 constexpr uint32_t kSpecMaxSteps = 24;  // ... over wave slices of at most this many steps
 constexpr uint32_t kMaxChunks = 64;  // workgroups per row
+constexpr uint32_t kDefaultGroups = 512;   // chunking: small batches aim this high
+constexpr uint32_t kMaxGroups = 1024;      // chunking: eight per row up to this many
 constexpr uint32_t kLineWords = 32;  // u32 per 128-byte cache line (row counters)
 
 constexpr int32_t kStOk = 0;

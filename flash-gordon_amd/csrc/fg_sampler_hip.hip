@@ -140,7 +140,7 @@ struct fg_sampler_hip {
   uint32_t* d_row_done;     // [max_rows * kLineWords]
   uint32_t* d_nuc_deep;     // [max_rows]
   float* d_nuc_max;         // [max_rows]
-  uint32_t target_groups;   // workgroups per launch the chunking aims for
+  uint32_t target_groups;   // FG_HIP_TARGET_GROUPS, 0 = the built-in chunking rule
   uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
   uint64_t* counters;       // event counters, FG_SAMPLE_TRACE builds only
 };
@@ -408,14 +408,16 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   }
   s->vocab = vocab;
   s->max_rows = max_rows;
-  s->target_groups = 512u;
+  s->target_groups = 0u;  // 0: the built-in chunking rule
   if (const char* t = getenv("FG_HIP_TARGET_GROUPS")) {
     const long v = strtol(t, nullptr, 10);
     if (v >= 1 && v <= 1 << 20) s->target_groups = static_cast<uint32_t>(v);
   }
   hipError_t e = hipGetDevice(&s->device);
-  // rows * chunks(rows) <= target_groups + rows for every batch size.
-  const uint64_t slots = (static_cast<uint64_t>(s->target_groups) + max_rows) * fg::kWaves;
+  // rows * chunks(rows) <= max(target, kMaxGroups) + rows for every batch
+  // size.
+  const uint64_t groups_cap = s->target_groups > fg::kMaxGroups ? s->target_groups : fg::kMaxGroups;
+  const uint64_t slots = (groups_cap + max_rows) * fg::kWaves;
   s->slots = slots;
   s->h_params = static_cast<RowParams*>(calloc(max_rows, sizeof(RowParams)));
   if (!s->h_params) {
@@ -436,8 +438,8 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMalloc(&s->d_nuc_max, sizeof(float) * max_rows);
   if (e == hipSuccess) e = hipMemset(s->d_params, 0, sizeof(RowParams) * max_rows);
 #ifdef FG_SAMPLE_TRACE
-  if (e == hipSuccess) e = hipMalloc(&s->trace, sizeof(uint64_t) * 8u * (s->target_groups + max_rows));
-  if (e == hipSuccess) e = hipMemset(s->trace, 0, sizeof(uint64_t) * 8u * (s->target_groups + max_rows));
+  if (e == hipSuccess) e = hipMalloc(&s->trace, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
+  if (e == hipSuccess) e = hipMemset(s->trace, 0, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
   if (e == hipSuccess) e = hipMalloc(&s->counters, sizeof(uint64_t) * 16u);
   if (e == hipSuccess) e = hipMemset(s->counters, 0, sizeof(uint64_t) * 16u);
   if (e == hipSuccess)
@@ -508,9 +510,24 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
       (b->logprobs && (!b->logprob_values || !b->logprob_ids)))
     return arg_fail(err, "invalid sampled output arguments");
   const uint32_t vocab = s->vocab;
-  // Chunking: aim for target_groups workgroups, at most kMaxChunks per row,
-  // each wave slice a multiple of 4 elements.
-  uint32_t chunks = (s->target_groups + b->rows - 1u) / b->rows;
+  // Chunking (measured on MI355X, V = 151,936): at least ~512 workgroups
+  // for small batches (one row: 64 chunks); eight per row up to 1,024
+  // workgroups (slices of ~4.6 steps: config 2 at 64 rows and config 4 at
+  // 128 both run fastest there); a whole-row nucleus launch keeps ~512
+  // (its per-workgroup tail is heavier).  FG_HIP_TARGET_GROUPS overrides:
+  // ceil(target / rows) chunks.  At most kMaxChunks per row; each wave
+  // slice a multiple of 4 elements.
+  bool nuc_rows = false;
+  for (uint32_t r = 0; r < b->rows; r++)
+    nuc_rows |= s->h_params[r].temperature > 0.0f && s->h_params[r].top_k == 0u;
+  uint32_t chunks;
+  if (s->target_groups) {
+    chunks = (s->target_groups + b->rows - 1u) / b->rows;
+  } else {
+    const uint32_t wide = (fg::kDefaultGroups + b->rows - 1u) / b->rows;
+    const uint32_t per_row = fg::kMaxGroups / b->rows < 8u ? fg::kMaxGroups / b->rows : 8u;
+    chunks = nuc_rows || wide > per_row ? wide : per_row;
+  }
   if (chunks > fg::kMaxChunks) chunks = fg::kMaxChunks;
   if (chunks < 1u) chunks = 1u;
   const uint32_t waves = chunks * fg::kWaves;
