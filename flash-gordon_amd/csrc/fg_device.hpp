@@ -165,6 +165,19 @@ __device__ __forceinline__ uint32_t greedy_id(uint64_t c) { return ~static_cast<
 // Penalty of src/sampler.c:55-58 for one logit seen c > 0 times.  The kernels
 // are compiled with -ffp-contract=off so the product and the sum round
 // separately, and '/' is the IEEE-rounded f32 division.
+// The same value without branches: both the quotient and the product are
+// formed and one is selected (s / 1 and s * 1 are exact, so a repetition of
+// 1 needs no test); a zero count returns s.
+__device__ __forceinline__ float penalise_sel(float s, uint32_t c, float pres, float freq,
+                                              float rep) {
+  const float q = s / rep;
+  const float m = s * rep;
+  const float r = s > 0.0f ? q : m;
+  const float fc = freq * static_cast<float>(c);
+  const float total = fc + pres;
+  return c != 0u ? r - total : s;
+}
+
 __device__ __forceinline__ float penalise(float s, uint32_t c, float pres, float freq, float rep) {
   if (c == 0u) return s;
   if (rep != 1.0f) s = s > 0.0f ? s / rep : s * rep;

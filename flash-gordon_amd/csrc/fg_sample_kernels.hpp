@@ -147,7 +147,7 @@ constexpr uint64_t kRawTag = 1ull << 63;  // a staged raw entry; composites stay
 struct TopList {
   uint64_t top;    // lane i: i-th best composite
   uint64_t R;      // filter: a candidate must be > R (wave-uniform)
-  uint64_t* buf;   // kCap staged composites (wave-private LDS)
+  uint64_t* buf;   // kCap staged composites + one spare slot per lane (wave-private LDS)
   uint32_t n;      // staged entries (wave-uniform)
   uint32_t kk;     // entries of the list that matter (1..64)
   float fM;        // float form of R for elements later in the stream
@@ -277,15 +277,14 @@ __device__ __forceinline__ void top_stage(TopList& t, uint64_t comp) {
 // (id << 32 | float bits, marked by kRawTag) and becomes a composite when it
 // is drained: the per-element cost stays a compare, a count and one store.
 // +Inf passes the filter and is dropped at the drain (its key is 0).
-__device__ __forceinline__ void top_stage_stream(TopList& t, bool valid, float v, uint32_t id,
-                                                 float f) {
-  const bool pass = valid && v >= f;
-  const uint64_t m = ballot(pass);
+__device__ __forceinline__ void top_stage_stream(TopList& t, float v, uint32_t id, float f) {
+  const bool pass = v >= f;  // f is NaN for masked elements
+  const uint64_t m = __builtin_amdgcn_ballot_w64(pass);
   if (m == 0ull) return;
   FG_COUNT(1, static_cast<unsigned long long>(__popcll(m)));
-  if (pass)
-    t.buf[t.n + lanes_below(m)] =
-        kRawTag | (static_cast<uint64_t>(id) << 32) | __float_as_uint(v);
+  // Every lane stores: those that fail to their own spare slot past kCap.
+  const uint32_t slot = pass ? t.n + lanes_below(m) : kCap + lane_id();
+  t.buf[slot] = kRawTag | (static_cast<uint64_t>(id) << 32) | __float_as_uint(v);
   t.n += static_cast<uint32_t>(__popcll(m));
 }
 
@@ -608,16 +607,15 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
   }
   if (F::kPen && pen) {
     // Penalties touch only elements with a nonzero count (sparse): a 64-lane
-    // slot pays for the IEEE division only when one of its lanes needs it.
+    // slot pays for the IEEE division only when one of its lanes needs it,
+    // and then without branches.
 #pragma unroll
     for (int j = 0; j < kStepVec; j++) {
       const uint32_t c4[4] = {y[j].x, y[j].y, y[j].z, y[j].w};
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const bool nz = c4[e] != 0u;
-        if (ballot(nz) != 0ull) {
-          if (nz) v[j][e] = penalise(v[j][e], c4[e], p.presence, p.frequency, p.repetition);
-        }
+        if (__builtin_amdgcn_ballot_w64(c4[e] != 0u) != 0ull)
+          v[j][e] = penalise_sel(v[j][e], c4[e], p.presence, p.frequency, p.repetition);
       }
     }
   }
@@ -730,20 +728,22 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
     top_adopt(st.t);  // the workgroup's bound (the other waves' first steps too)
     // Most steps hold no candidate once the filter has risen: one ballot on
     // the lane maxima skips the per-element staging.
+    // +Inf counts here (it is dropped where it is drained); NaN does not.
     float lane_max = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++)
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (ok[j] && v[j][e] < INFINITY) lane_max = fmaxf(lane_max, v[j][e]);
+    for (int j = 0; j < kStepVec; j++) {
+      const float m = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
+      lane_max = ok[j] ? fmaxf(lane_max, m) : lane_max;
+    }
     const float f = F::kSpec ? fmaxf(st.t.fM, st.fS) : st.t.fM;
     if (ballot(lane_max >= f) != 0ull) {
       FG_COUNT(2, 1ull);
 #pragma unroll
       for (int j = 0; j < kStepVec; j++) {
         const uint32_t q = q0 + j * kWave + lane;
+        const float fj = ok[j] ? f : __builtin_nanf("");
 #pragma unroll
-        for (int e = 0; e < 4; e++) top_stage_stream(st.t, ok[j], v[j][e], q * 4u + e, f);
+        for (int e = 0; e < 4; e++) top_stage_stream(st.t, v[j][e], q * 4u + e, fj);
       }
       top_drain(st.t, false);
     }
@@ -835,7 +835,7 @@ __device__ inline uint64_t spec_check(const SampleArgs& a, const RowParams& p, u
 
 template <class F>
 __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
-  __shared__ uint64_t s_buf[F::kTop ? kWaves : 1][F::kTop ? kCap : 1];
+  __shared__ uint64_t s_buf[F::kTop ? kWaves : 1][F::kTop ? kCap + kWave : 1];
   __shared__ uint64_t s_top[kWaves][kWave];
   __shared__ uint64_t s_greedy[kWaves];
   __shared__ uint32_t s_ks[kWaves];
