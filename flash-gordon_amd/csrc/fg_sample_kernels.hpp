@@ -687,17 +687,29 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
     st.ne += static_cast<double>(ef);
   }
   if (F::kTop && st.t.kk) {
+    // The lane's largest value: +Inf counts here (it is dropped where it is
+    // drained); NaN does not.
+    float lane_max = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kStepVec; j++) {
+      const float m = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
+      lane_max = ok[j] ? fmaxf(lane_max, m) : lane_max;
+    }
     if (st.first) {
       // The kk-th largest lane maximum: at least kk keys of this step are >=
-      // it, so it bounds the wave's kk-th key from below.
-      uint32_t lane_max_key = 0u;
+      // it, so it bounds the wave's kk-th key from below.  A lane whose
+      // largest value is +Inf takes its largest finite key the long way.
+      uint32_t lane_max_key = float_key(lane_max);
+      if (ballot(lane_max == INFINITY) != 0ull) {
+        lane_max_key = 0u;
 #pragma unroll
-      for (int j = 0; j < kStepVec; j++)
+        for (int j = 0; j < kStepVec; j++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
-          lane_max_key = key > lane_max_key ? key : lane_max_key;
-        }
+          for (int e = 0; e < 4; e++) {
+            const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
+            lane_max_key = key > lane_max_key ? key : lane_max_key;
+          }
+      }
       // Largest T (to 2^12 key units) with at least kk lane maxima >= T: a
       // ballot radix search, cheaper than sorting the 64 maxima.
       uint32_t T = 0u;
@@ -727,14 +739,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
     }
     top_adopt(st.t);  // the workgroup's bound (the other waves' first steps too)
     // Most steps hold no candidate once the filter has risen: one ballot on
-    // the lane maxima skips the per-element staging.
-    // +Inf counts here (it is dropped where it is drained); NaN does not.
-    float lane_max = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kStepVec; j++) {
-      const float m = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
-      lane_max = ok[j] ? fmaxf(lane_max, m) : lane_max;
-    }
+    // the lane maxima (computed above) skips the per-element staging.
     const float f = F::kSpec ? fmaxf(st.t.fM, st.fS) : st.t.fM;
     if (ballot(lane_max >= f) != 0ull) {
       FG_COUNT(2, 1ull);
