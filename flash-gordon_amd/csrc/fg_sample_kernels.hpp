@@ -417,8 +417,13 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
       const double v = live ? static_cast<double>(key_to_float(comp_key(sorted))) : 0.0;
       const double vmax = __longlong_as_double(static_cast<long long>(
           readlane64(static_cast<uint64_t>(__double_as_longlong(v)), 0)));
+      // Both running sums at once (independent chains): the tempered one is
+      // read at the cut, and a prefix sum up to a lane ignores later lanes.
+      const double inv_t = 1.0 / static_cast<double>(p.temperature);
       const double e = live ? exp(v - vmax) : 0.0;
+      const double te = live ? exp((v - vmax) * inv_t) : 0.0;
       const double ecum = wave_prefix_sum_f64(e);
+      const double tcum = wave_prefix_sum_f64(te);
       double sum = __longlong_as_double(static_cast<long long>(
           readlane64(static_cast<uint64_t>(__double_as_longlong(ecum)), limit - 1u)));
       // Relative error bound of the f32-term mass (see Mass).
@@ -438,16 +443,15 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
         // A deeper cut, or a list that ends on zeros (where key order, +0
         // above -0, and value order, 0 == -0, may keep different entries),
         // is left to the deep-row kernel.
-        const uint32_t edge_key = comp_key(readlane64(fin, kMaxK - 1u));
-        const bool zero_edge = edge_key == 0x7fffffffu || edge_key == 0x80000000u;
-        // So is a cut that the mass's error bound could move: the positions
-        // either side of the cut must clear top_p by twice the bound.
-        const double gap = lane < cutoff ? fabs(ecum - target) / sum : INFINITY;
-        const bool close = -wave_max_f64(-gap) <= 2.0 * bound;
-        if (nuc && !whole_row_listed && (hit == 0ull || zero_edge || close)) status = kStLimit;
-        const double inv_t = 1.0 / static_cast<double>(p.temperature);
-        const double te = lane < cutoff ? exp((v - vmax) * inv_t) : 0.0;
-        const double tcum = wave_prefix_sum_f64(te);
+        if (nuc && !whole_row_listed) {
+          const uint32_t edge_key = comp_key(readlane64(fin, kMaxK - 1u));
+          const bool zero_edge = edge_key == 0x7fffffffu || edge_key == 0x80000000u;
+          // So is a cut that the mass's error bound could move: the positions
+          // either side of the cut must clear top_p by twice the bound.
+          const double gap = lane < cutoff ? fabs(ecum - target) / sum : INFINITY;
+          const bool close = -wave_max_f64(-gap) <= 2.0 * bound;
+          if (hit == 0ull || zero_edge || close) status = kStLimit;
+        }
         const double tsum = __longlong_as_double(static_cast<long long>(
             readlane64(static_cast<uint64_t>(__double_as_longlong(tcum)), cutoff - 1u)));
         if (status != kStOk) {
