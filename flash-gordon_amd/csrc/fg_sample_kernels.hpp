@@ -542,9 +542,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const void* base, u
 }
 __device__ __forceinline__ void load_quad_buf(__amdgpu_buffer_rsrc_t rl, __amdgpu_buffer_rsrc_t rc,
                                               bool pen, uint32_t qrel, f4& x, u4& y) {
+  // Counts are always loaded: without penalties rc has no records, so the
+  // load returns zeros without touching memory (and needs no branch).
+  (void)pen;
   x = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rl, qrel * 16u, 0, kLoadNT));
-  y = pen ? __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rc, qrel * 16u, 0, kLoadNT))
-          : u4{0u, 0u, 0u, 0u};
+  y = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rc, qrel * 16u, 0, kLoadNT));
 }
 
 struct WaveState {
@@ -910,7 +912,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     const uint32_t slice_bytes = (q_end - q_begin) * 16u;
     const __amdgpu_buffer_rsrc_t rl = slice_rsrc(lrow + 4u * q_begin, slice_bytes);
     const __amdgpu_buffer_rsrc_t rc =
-        slice_rsrc(cnt ? static_cast<const void*>(crow + 4u * q_begin) : lrow, slice_bytes);
+        slice_rsrc(cnt ? static_cast<const void*>(crow + 4u * q_begin) : lrow, cnt ? slice_bytes : 0u);
     auto load = [&](f4 (&x)[kStepVec], u4 (&y)[kStepVec], uint32_t qs) {
 #pragma unroll
       for (int j = 0; j < kStepVec; j++) {
