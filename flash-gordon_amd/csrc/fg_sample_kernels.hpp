@@ -1038,28 +1038,69 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     // ---- last workgroup of the row: merge the other workgroups' lists ----
     const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
     if (F::kTop && kk) {
-      // Eight lists per round, loaded together and merged as a tree of
-      // side-by-side pairs; this workgroup's own list is already in `fin`.
-      for (uint32_t c0 = 0; c0 < a.chunks; c0 += 8u) {
-        uint64_t x[8];
+      if (kk <= 32u) {
+        // Lists of at most 32: two per register, the second loaded in
+        // reverse into lanes 32-63, so a pair is already a bitonic sequence
+        // and one 64-wide merge stage leaves the pair's best 32 in lanes
+        // 0-31.  Eight lists per round (this workgroup's own included) in
+        // three levels; rounds fold into `fin`.
+        const bool hi = lane >= 32u;
+        const uint32_t pos = hi ? 63u - lane : lane;  // list position this lane holds
+        uint64_t acc = 0ull;
+        for (uint32_t c0 = 0; c0 < a.chunks; c0 += 8u) {
+          uint64_t x[4];
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-          const uint32_t c = c0 + t;
-          x[t] = (c < a.chunks && c != chunk && lane < kk)
-                     ? load_coherent(a.cand + (row_slot + c) * kMaxK + lane)
-                     : 0ull;
+          for (int t = 0; t < 4; t++) {
+            const uint32_t c = c0 + 2u * t + (hi ? 1u : 0u);
+            x[t] = (c < a.chunks && pos < kk)
+                       ? load_coherent(a.cand + (row_slot + c) * kMaxK + pos)
+                       : 0ull;
+          }
+          if (spec && c0 == 0u) {
+            // The waves' speculative keys travel with the first lists (the
+            // asm keeps the load here instead of after the merges).
+            ks0 = spec_key(a, row, lane, s_ks);
+            asm volatile("" ::"v"(ks0));
+          }
+#pragma unroll
+          for (int t = 0; t < 4; t++) x[t] = bitonic_merge_stage<64>(x[t]);
+          // The reversals run in every lane (a cross-lane read from a lane
+          // that is switched off would not return its value), then select.
+          const uint64_t r1 = lane_reverse64(x[1]), r3 = lane_reverse64(x[3]);
+          x[0] = bitonic_merge_stage<64>(hi ? r1 : x[0]);
+          x[2] = bitonic_merge_stage<64>(hi ? r3 : x[2]);
+          const uint64_t r2 = lane_reverse64(x[2]);
+          x[0] = bitonic_merge_stage<64>(hi ? r2 : x[0]);
+          if (c0 == 0u) {
+            acc = x[0];
+          } else {
+            const uint64_t r0 = lane_reverse64(x[0]);
+            acc = bitonic_merge_stage<64>(hi ? r0 : acc);
+          }
         }
-        if (spec && c0 == 0u) {
-          // The waves' speculative keys travel with the first lists (the
-          // asm keeps the load here instead of after the merges).
-          ks0 = spec_key(a, row, lane, s_ks);
-          asm volatile("" ::"v"(ks0));
+        fin = acc;
+      } else {
+        // Eight lists per round, loaded together and merged as a tree of
+        // side-by-side pairs; this workgroup's own list is already in `fin`.
+        for (uint32_t c0 = 0; c0 < a.chunks; c0 += 8u) {
+          uint64_t x[8];
+#pragma unroll
+          for (int t = 0; t < 8; t++) {
+            const uint32_t c = c0 + t;
+            x[t] = (c < a.chunks && c != chunk && lane < kk)
+                       ? load_coherent(a.cand + (row_slot + c) * kMaxK + lane)
+                       : 0ull;
+          }
+          if (spec && c0 == 0u) {
+            ks0 = spec_key(a, row, lane, s_ks);
+            asm volatile("" ::"v"(ks0));
+          }
+          wave_merge_desc2(x[0], x[1], x[2], x[3]);
+          wave_merge_desc2(x[4], x[5], x[6], x[7]);
+          wave_merge_desc2(x[0], x[2], x[4], x[6]);
+          wave_merge_desc2(fin, x[0], x[4], 0ull);
+          if (readlane64(x[4], 0) > readlane64(fin, kk - 1u)) fin = wave_merge_desc(fin, x[4]);
         }
-        wave_merge_desc2(x[0], x[1], x[2], x[3]);
-        wave_merge_desc2(x[4], x[5], x[6], x[7]);
-        wave_merge_desc2(x[0], x[2], x[4], x[6]);
-        wave_merge_desc2(fin, x[0], x[4], 0ull);
-        if (readlane64(x[4], 0) > readlane64(fin, kk - 1u)) fin = wave_merge_desc(fin, x[4]);
       }
       FG_TRACE(a, 5);
     }
