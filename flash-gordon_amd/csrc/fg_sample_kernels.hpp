@@ -996,10 +996,23 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   double m = -INFINITY, z = 0.0;
   Mass zs{-INFINITY, 0.0, 0.0};
   if (F::kTop && kk) {
-    // (0,1) and (2,3) side by side, then the two results.
-    uint64_t a0 = s_top[0][lane], a1 = s_top[2][lane];
-    wave_merge_desc2(a0, s_top[1][lane], a1, s_top[3][lane]);
-    fin = readlane64(a1, 0) > readlane64(a0, kk - 1u) ? wave_merge_desc(a0, a1) : a0;
+    if (kk <= 32u) {
+      // Two lists per register, the second read in reverse into lanes
+      // 32-63 (a bitonic pair), then the two results the same way.
+      const bool hi = lane >= 32u;
+      const uint32_t pos = hi ? 63u - lane : lane;
+      uint64_t a0 = hi ? s_top[1][pos] : s_top[0][pos];
+      uint64_t a1 = hi ? s_top[3][pos] : s_top[2][pos];
+      a0 = bitonic_merge_stage<64>(a0);
+      a1 = bitonic_merge_stage<64>(a1);
+      const uint64_t r1 = lane_reverse64(a1);
+      fin = bitonic_merge_stage<64>(hi ? r1 : a0);
+    } else {
+      // (0,1) and (2,3) side by side, then the two results.
+      uint64_t a0 = s_top[0][lane], a1 = s_top[2][lane];
+      wave_merge_desc2(a0, s_top[1][lane], a1, s_top[3][lane]);
+      fin = readlane64(a1, 0) > readlane64(a0, kk - 1u) ? wave_merge_desc(a0, a1) : a0;
+    }
   }
   for (int w = 0; w < kWaves; w++) {
     g = s_greedy[w] > g ? s_greedy[w] : g;
