@@ -49,6 +49,7 @@ constexpr uint32_t kStepElems = kStepQuads * 4u;
 // LDS staging per wave: fewer than 64 left over plus one full step.
 constexpr uint32_t kCap = 64u + kStepElems;
 constexpr uint32_t kMaxK = 64;       // largest top-k / log-prob count
+constexpr uint32_t kXcds = 8;  // XCDs of an MI355X (workgroups go round robin)
 constexpr uint32_t kSpecMinK = 32;   // top lists longer than this stage speculatively
 constexpr uint32_t kSpecMaxSteps = 24;  // ... over wave slices of at most this many steps
 constexpr uint32_t kMaxChunks = 64;  // workgroups per row
@@ -863,8 +864,26 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   // waterfall loop).
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t lane = lane_id();
-  const uint32_t row = blockIdx.x / a.chunks;
-  const uint32_t chunk = blockIdx.x - row * a.chunks;
+  // A row's chunks share one XCD (and its L2): the dispatcher hands
+  // workgroups to the kXcds XCDs round robin, so chunk c of row r takes
+  // blockIdx (r / kXcds) * chunks * kXcds + c * kXcds + r % kXcds.  Rows past
+  // the last whole group of kXcds are laid out row-major after them.  Only
+  // speed depends on the dispatch order; any order is correct.
+  uint32_t row, chunk;
+  {
+    const uint32_t b = blockIdx.x;
+    const uint32_t grouped = a.rows - a.rows % kXcds;
+    if (b < grouped * a.chunks) {
+      const uint32_t q = b / kXcds;
+      const uint32_t g = q / a.chunks;
+      row = g * kXcds + b % kXcds;
+      chunk = q - g * a.chunks;
+    } else {
+      const uint32_t r = (b - grouped * a.chunks) / a.chunks;
+      row = grouped + r;
+      chunk = b - grouped * a.chunks - r * a.chunks;
+    }
+  }
   const RowParams p = a.params[row];
   const float urow = a.uniforms[row];  // early: the row's last step needs it
   const bool greedy = p.temperature == 0.0f;
