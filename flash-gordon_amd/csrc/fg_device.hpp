@@ -415,8 +415,11 @@ __device__ __forceinline__ double wave_prefix_sum_f64(double x) {
   const double r0 = __longlong_as_double(static_cast<long long>(readlane64(b, 15)));
   const double r1 = __longlong_as_double(static_cast<long long>(readlane64(b, 31)));
   const double r2 = __longlong_as_double(static_cast<long long>(readlane64(b, 47)));
+  // The rows' offsets without branches: 0, r0, r0 + r1, (r0 + r1) + r2.
   const uint32_t row = lane_id() >> 4;
-  const double before = row == 0 ? 0.0 : row == 1 ? r0 : row == 2 ? r0 + r1 : (r0 + r1) + r2;
+  const double r01 = r0 + r1;
+  const double r012 = r01 + r2;
+  const double before = row < 2u ? (row == 0u ? 0.0 : r0) : (row == 2u ? r01 : r012);
   return x + before;
 }
 

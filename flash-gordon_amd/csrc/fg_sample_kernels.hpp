@@ -370,7 +370,8 @@ __device__ __forceinline__ Mass wave_mass_combine(double m, double z, double e) 
 // whole-row nucleus.  Writes token, logit, status and log-probs.
 __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint32_t row,
                                   uint64_t fin, uint64_t gbest, double m, double z, Mass zs,
-                                  const float* lrow, const uint32_t* crow, bool pen, float u) {
+                                  const float* lrow, const uint32_t* crow, bool pen, float u,
+                                  double inv_t) {
   const uint32_t lane = lane_id();
   const bool greedy = p.temperature == 0.0f;
   const uint32_t L = a.logprobs;
@@ -420,9 +421,11 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
           readlane64(static_cast<uint64_t>(__double_as_longlong(v)), 0)));
       // Both running sums at once (independent chains): the tempered one is
       // read at the cut, and a prefix sum up to a lane ignores later lanes.
-      const double inv_t = 1.0 / static_cast<double>(p.temperature);
-      const double e = live ? exp(v - vmax) : 0.0;
-      const double te = live ? exp((v - vmax) * inv_t) : 0.0;
+      // Every lane runs both exps (exp(-inf) = 0 past the list), so the two
+      // chains interleave instead of running one after the other.
+      const double d = live ? v - vmax : -INFINITY;
+      const double e = exp(d);
+      const double te = exp(d * inv_t);
       const double ecum = wave_prefix_sum_f64(e);
       const double tcum = wave_prefix_sum_f64(te);
       double sum = __longlong_as_double(static_cast<long long>(
@@ -901,6 +904,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
                     a.wave_elems <= kSpecMaxSteps * kStepElems;
   const float t_eff = p.temperature > 0.0f ? p.temperature : 1.0f;
   const float log2e_over_t = 1.4426950408889634f / t_eff;
+  // 1 / T for the finish, divided here where the loads' latency hides it.
+  const double inv_t = 1.0 / static_cast<double>(p.temperature);
 
   const float* lrow = a.logits + static_cast<uint64_t>(row) * a.lstride;
   const uint32_t* crow = pen ? a.counts + static_cast<uint64_t>(row) * a.cstride : nullptr;
@@ -1162,7 +1167,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   // One copy of the check and of the finish serves both paths.
   if (spec) fin = spec_check(a, p, row, pen, lrow, crow, fin, kk, s_ks, ks0, s_buf[0], &s_wg_key);
   FG_TRACE(a, 6);
-  finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow);
+  finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
   if (a.chunks != 1u && lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
   FG_TRACE(a, 7);
 }
