@@ -956,14 +956,34 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       }
     };
     load(xa, ya, q_begin);
+    // Fair progress between the waves sharing a SIMD: a wave starts at the
+    // highest issue priority and steps down at each quarter of its slice, so
+    // a wave that has fallen behind (the hardware favours older waves at
+    // equal priority) is issued first until it catches up.
+    const uint32_t quarter = (q_end - q_begin + 3u) / 4u;
+    uint32_t next_drop = q_begin + quarter;
+    uint32_t level = 3u;
+    __builtin_amdgcn_s_setprio(3);
+    auto pace = [&](uint32_t q) {
+      if (q >= next_drop) {
+        next_drop += quarter;
+        level--;
+        if (level == 2u) __builtin_amdgcn_s_setprio(2);
+        else if (level == 1u) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      }
+    };
     for (uint32_t q0 = q_begin;;) {
       load(xb, yb, q0 + kStepQuads);
       process_step<F>(st, p, pen, greedy, lse, nuc, spec, log2e_over_t, prow, xa, ya, q0, q_end);
       if ((q0 += kStepQuads) >= q_end) break;
+      pace(q0);
       load(xa, ya, q0 + kStepQuads);
       process_step<F>(st, p, pen, greedy, lse, nuc, spec, log2e_over_t, prow, xb, yb, q0, q_end);
       if ((q0 += kStepQuads) >= q_end) break;
+      pace(q0);
     }
+    __builtin_amdgcn_s_setprio(3);  // the rest of the kernel is the row's critical path
   }
   {
     // Fewer than 4 trailing elements (only at the end of a row): lane 0.
