@@ -53,8 +53,8 @@ constexpr uint32_t kXcds = 8;  // XCDs of an MI355X (workgroups go round robin)
 constexpr uint32_t kSpecMinK = 32;   // top lists longer than this stage speculatively
 constexpr uint32_t kSpecMaxSteps = 24;  // ... over wave slices of at most this many steps
 constexpr uint32_t kMaxChunks = 64;  // workgroups per row
-constexpr uint32_t kDefaultGroups = 512;   // chunking: small batches aim this high
-constexpr uint32_t kMaxGroups = 1024;      // chunking: eight per row up to this many
+constexpr uint32_t kDefaultGroups = 512;   // chunking: ceil(512 / rows) chunks per row
+constexpr uint32_t kMaxGroups = 1024;      // workspace: workgroups a launch may use beyond rows
 constexpr uint32_t kLineWords = 32;  // u32 per 128-byte cache line (row counters)
 
 constexpr int32_t kStOk = 0;
@@ -72,7 +72,11 @@ struct SampleArgs {
   uint32_t vocab;
   uint32_t rows;
   uint32_t chunks;      // workgroups per row
-  uint32_t wave_elems;  // elements per wave slice (multiple of 4)
+  uint32_t wave_elems;  // elements per wave slice of chunks < split (multiple of 4)
+  uint32_t wave_elems_b;  // elements per wave slice of chunks >= split (multiple of 4)
+  uint32_t pace;          // 1: waves step their issue priority down as they progress
+  uint32_t split;         // chunks [0, split) run in the grid's first half, the
+                          // rest in its second half (split == chunks: one layout)
   uint32_t logprobs;
   uint32_t* tokens;
   float* token_logits;
@@ -776,6 +780,18 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
 
 // ---- speculation check ------------------------------------------------------
 
+// Wave slice i of a row (i = chunk * kWaves + wave): [begin, begin + len)
+// clipped to the vocabulary.
+__device__ __forceinline__ uint32_t slice_begin(const SampleArgs& a, uint32_t i) {
+  const uint32_t na = a.split * kWaves;
+  const uint32_t b = i < na ? i * a.wave_elems : na * a.wave_elems + (i - na) * a.wave_elems_b;
+  return min(b, a.vocab);
+}
+__device__ __forceinline__ uint32_t slice_end(const SampleArgs& a, uint32_t i) {
+  const uint32_t len = i < a.split * kWaves ? a.wave_elems : a.wave_elems_b;
+  return min(slice_begin(a, i) + len, a.vocab);
+}
+
 // Reads wave slice `i` of the row again and merges into `fin` (the row's list)
 // the elements the wave skipped under its speculative key ks that beat the
 // list's kk-th entry.  One wave; `buf` is its free staging LDS.
@@ -784,8 +800,8 @@ __device__ inline uint64_t rescan_slice(const SampleArgs& a, const RowParams& p,
                                         uint32_t kk, uint32_t ks, uint32_t i, uint64_t* buf,
                                         uint32_t* wg_key) {
   const uint32_t lane = lane_id();
-  const uint32_t wbegin = min(i * a.wave_elems, a.vocab);
-  const uint32_t wend = min(wbegin + a.wave_elems, a.vocab);
+  const uint32_t wbegin = slice_begin(a, i);
+  const uint32_t wend = slice_end(a, i);
   const float fS = ks >= 0x00800000u ? key_to_float(ks) : -3.402823466e38f;
   const uint64_t kth = readlane64(fin, kk - 1u);
   // shared = all ones: this list never publishes a workgroup bound.
@@ -877,15 +893,27 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t lane = lane_id();
   // A row's chunks share one XCD (and its L2): the dispatcher hands
-  // workgroups to the kXcds XCDs round robin, so chunk c of row r takes
-  // blockIdx (r / kXcds) * chunks * kXcds + c * kXcds + r % kXcds.  Rows past
+  // workgroups to the kXcds XCDs round robin, so row r's chunks take blockIdx
+  // values of residue r % kXcds.  With split < chunks (rows a multiple of
+  // kXcds, two halves of chunks) chunks [0, split) sit in the grid's first
+  // half and the rest in its second: the first-dispatched workgroup of a CU
+  // streams faster than the second, so its slices are made longer.  Rows past
   // the last whole group of kXcds are laid out row-major after them.  Only
   // speed depends on the dispatch order; any order is correct.
   uint32_t row, chunk;
   {
     const uint32_t b = blockIdx.x;
     const uint32_t grouped = a.rows - a.rows % kXcds;
-    if (b < grouped * a.chunks) {
+    if (a.split < a.chunks) {
+      const uint32_t half = a.rows * a.split;  // workgroups per half
+      const bool second = b >= half;
+      const uint32_t bb = second ? b - half : b;
+      const uint32_t hc = second ? a.chunks - a.split : a.split;
+      const uint32_t q = bb / kXcds;
+      const uint32_t g = q / hc;
+      row = g * kXcds + bb % kXcds;
+      chunk = q - g * hc + (second ? a.split : 0u);
+    } else if (b < grouped * a.chunks) {
       const uint32_t q = b / kXcds;
       const uint32_t g = q / a.chunks;
       row = g * kXcds + b % kXcds;
@@ -910,7 +938,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   // slices the exact filter soon passes it, and a check that fails would
   // read a long slice again.
   const bool spec = F::kSpec && !greedy && kk > kSpecMinK &&
-                    a.wave_elems <= kSpecMaxSteps * kStepElems;
+                    max(a.wave_elems, a.wave_elems_b) <= kSpecMaxSteps * kStepElems;
   const float t_eff = p.temperature > 0.0f ? p.temperature : 1.0f;
   const float log2e_over_t = 1.4426950408889634f / t_eff;
   // 1 / T for the finish, divided here where the loads' latency hides it.
@@ -920,8 +948,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint32_t* crow = pen ? a.counts + static_cast<uint64_t>(row) * a.cstride : nullptr;
   float* prow = a.penalised ? a.penalised + static_cast<uint64_t>(row) * a.vocab : nullptr;
 
-  const uint32_t wbegin = min((chunk * kWaves + wave) * a.wave_elems, a.vocab);
-  const uint32_t wend = min(wbegin + a.wave_elems, a.vocab);
+  const uint32_t wbegin = slice_begin(a, chunk * kWaves + wave);
+  const uint32_t wend = slice_end(a, chunk * kWaves + wave);
   const uint32_t q_begin = wbegin / 4u;
   const uint32_t q_end = (wbegin + ((wend - wbegin) & ~3u)) / 4u;
 
@@ -961,9 +989,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     // a wave that has fallen behind (the hardware favours older waves at
     // equal priority) is issued first until it catches up.
     const uint32_t quarter = (q_end - q_begin + 3u) / 4u;
-    uint32_t next_drop = q_begin + quarter;
+    uint32_t next_drop = a.pace ? q_begin + quarter : 0xffffffffu;
     uint32_t level = 3u;
-    __builtin_amdgcn_s_setprio(3);
+    if (a.pace) __builtin_amdgcn_s_setprio(3);
     auto pace = [&](uint32_t q) {
       if (q >= next_drop) {
         next_drop += quarter;
@@ -983,7 +1011,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       if ((q0 += kStepQuads) >= q_end) break;
       pace(q0);
     }
-    __builtin_amdgcn_s_setprio(3);  // the rest of the kernel is the row's critical path
+    if (a.pace) __builtin_amdgcn_s_setprio(3);  // the rest is the row's critical path
   }
   {
     // Fewer than 4 trailing elements (only at the end of a row): lane 0.

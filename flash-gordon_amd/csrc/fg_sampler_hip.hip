@@ -124,6 +124,16 @@ hipError_t dense_launch(fg::DenseArgs a, uint32_t tokens, hipStream_t stream) {
 
 }  // namespace
 
+// Paired layout (a row's chunks split between the grid's halves) for grids
+// of at most this many workgroups (two per CU), and the share (per mille) of
+// a row its first-half chunks stream: measured on MI355X at V = 151,936,
+// 580 for two chunks per row (config 3: 79.5 -> 77.4 us), even for more
+// (config 2: 21.96 -> 21.67 us); grids of four workgroups per CU run slower
+// paired (config 4: 28.5 -> 30.8 us).
+constexpr uint32_t kPairedMaxGroups = 512u;
+constexpr uint32_t kFrontPermilleTwo = 580u;
+constexpr uint32_t kFrontPermilleMany = 500u;
+
 struct fg_sampler_hip {
   int device;
   uint32_t vocab;
@@ -141,6 +151,9 @@ struct fg_sampler_hip {
   uint32_t* d_nuc_deep;     // [max_rows]
   float* d_nuc_max;         // [max_rows]
   uint32_t target_groups;   // FG_HIP_TARGET_GROUPS, 0 = the built-in chunking rule
+  uint32_t front_permille;  // FG_HIP_FRONT_SHARE: first-half share override, 0 = the rule
+  int32_t paired_override;  // FG_HIP_PAIRED: 0 / 1 forces the layout, -1 = the rule
+  int32_t pace_override;    // FG_HIP_PACE: 0 / 1 forces priority pacing, -1 = the rule
   uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
   uint64_t* counters;       // event counters, FG_SAMPLE_TRACE builds only
 };
@@ -413,6 +426,15 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
     const long v = strtol(t, nullptr, 10);
     if (v >= 1 && v <= 1 << 20) s->target_groups = static_cast<uint32_t>(v);
   }
+  s->front_permille = 0u;
+  s->paired_override = -1;
+  s->pace_override = -1;
+  if (const char* t = getenv("FG_HIP_PAIRED")) s->paired_override = atoi(t) != 0;
+  if (const char* t = getenv("FG_HIP_PACE")) s->pace_override = atoi(t) != 0;
+  if (const char* t = getenv("FG_HIP_FRONT_SHARE")) {
+    const long v = strtol(t, nullptr, 10);
+    if (v >= 500 && v < 750) s->front_permille = static_cast<uint32_t>(v);
+  }
   hipError_t e = hipGetDevice(&s->device);
   // rows * chunks(rows) <= max(target, kMaxGroups) + rows for every batch
   // size.
@@ -510,24 +532,16 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
       (b->logprobs && (!b->logprob_values || !b->logprob_ids)))
     return arg_fail(err, "invalid sampled output arguments");
   const uint32_t vocab = s->vocab;
-  // Chunking (measured on MI355X, V = 151,936): at least ~512 workgroups
-  // for small batches (one row: 64 chunks); eight per row up to 1,024
-  // workgroups (slices of ~4.6 steps: config 2 at 64 rows and config 4 at
-  // 128 both run fastest there); a whole-row nucleus launch keeps ~512
-  // (its per-workgroup tail is heavier).  FG_HIP_TARGET_GROUPS overrides:
-  // ceil(target / rows) chunks.  At most kMaxChunks per row; each wave
-  // slice a multiple of 4 elements.
-  bool nuc_rows = false;
-  for (uint32_t r = 0; r < b->rows; r++)
-    nuc_rows |= s->h_params[r].temperature > 0.0f && s->h_params[r].top_k == 0u;
-  uint32_t chunks;
-  if (s->target_groups) {
-    chunks = (s->target_groups + b->rows - 1u) / b->rows;
-  } else {
-    const uint32_t wide = (fg::kDefaultGroups + b->rows - 1u) / b->rows;
-    const uint32_t per_row = fg::kMaxGroups / b->rows < 8u ? fg::kMaxGroups / b->rows : 8u;
-    chunks = nuc_rows || wide > per_row ? wide : per_row;
-  }
+  // Chunking (measured on MI355X, V = 151,936): ceil(512 / rows) chunks,
+  // two workgroups per CU (config 2's 64 rows: 8 chunks; config 3's 256: 2;
+  // config 4's 128 rows: 4 chunks 28.1 us against 8 chunks 29.9-31.1; one
+  // row: 64).  FG_HIP_TARGET_GROUPS overrides: ceil(target / rows) chunks.
+  // At most kMaxChunks per row; each wave slice a multiple of 4 elements.
+  bool same_cost = true;  // every row alike in penalties (for the paired layout)
+  for (uint32_t r = 1; r < b->rows; r++)
+    same_cost &= ((s->h_params[r].flags ^ s->h_params[0].flags) & fg::kRowPenalties) == 0u;
+  const uint32_t target = s->target_groups ? s->target_groups : fg::kDefaultGroups;
+  uint32_t chunks = (target + b->rows - 1u) / b->rows;
   if (chunks > fg::kMaxChunks) chunks = fg::kMaxChunks;
   if (chunks < 1u) chunks = 1u;
   const uint32_t waves = chunks * fg::kWaves;
@@ -551,6 +565,35 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
   a.rows = b->rows;
   a.chunks = chunks;
   a.wave_elems = wave_elems;
+  a.wave_elems_b = wave_elems;
+  a.split = chunks;
+  // The first workgroup dispatched to a CU streams faster than the second
+  // (measured: ~8% at 8 chunks of V = 151,936 per row, ~12% at 2).  With
+  // the rows a multiple of the XCD count, an even chunk count and at most
+  // two workgroups per CU, a row's first chunks go to the grid's first half
+  // (longer slices at two chunks per row), the others to its second half.
+  a.pace = s->pace_override >= 0 ? static_cast<uint32_t>(s->pace_override) : 1u;
+  // Rows of unlike cost keep the row-major halves: the costlier rows (first
+  // in the batch) then run in the faster first half (config 4, penalties on
+  // rows 0-63 only: 28.1 us against 30.2 paired).
+  const bool paired_rule =
+      same_cost && static_cast<uint64_t>(b->rows) * chunks <= kPairedMaxGroups;
+  if (b->rows % fg::kXcds == 0u && chunks % 2u == 0u &&
+      (s->paired_override >= 0 ? s->paired_override != 0 : paired_rule)) {
+    const uint32_t permille = s->front_permille ? s->front_permille
+                              : chunks == 2u    ? kFrontPermilleTwo
+                                                : kFrontPermilleMany;
+    const uint32_t na = chunks / 2u * fg::kWaves;
+    uint64_t ea = (static_cast<uint64_t>(vocab) * permille + 1000u * na - 1u) / (1000u * na);
+    ea = (ea + 3u) & ~3ull;
+    if (ea * na < vocab) {
+      uint64_t eb = (vocab - ea * na + na - 1u) / na;
+      eb = (eb + 3u) & ~3ull;
+      a.wave_elems = static_cast<uint32_t>(ea);
+      a.wave_elems_b = static_cast<uint32_t>(eb);
+      a.split = chunks / 2u;
+    }
+  }
   a.logprobs = b->logprobs;
   a.tokens = b->tokens;
   a.token_logits = b->token_logits;
@@ -570,7 +613,7 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
 
   // The vector path addresses a slice with 32-bit byte offsets.
   const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
-                   wave_elems < (1u << 28) &&
+                   a.wave_elems < (1u << 28) && a.wave_elems_b < (1u << 28) &&
                    (!b->counts || (aligned16(b->counts) && (b->counts_stride % 4u) == 0u));
   bool any_pen = false, any_greedy = false, any_top = b->logprobs != 0u, any_nuc = false;
   bool any_spec = false;

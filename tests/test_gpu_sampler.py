@@ -367,3 +367,39 @@ def test_speculative_filter_rescans(dev, k, logprobs):
     else:
         check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), W.oracle_run(w),
               "speculation nucleus", NUC_BOUNDARY)
+
+
+@pytest.mark.parametrize("groups,share,k", [(32, 650, 20), (32, 650, 64), (32, 650, 0),
+                                            (128, 500, 20), (128, 600, 64), (128, 560, 0)])
+def test_paired_layout_shares(dev, monkeypatch, groups, share, k):
+    """The paired layout (a row's first chunks in the grid's first half, with
+    a larger share of the row, the rest in its second half): 16 rows, 2 or 8
+    chunks per row, uneven slices; rows whose best values sit at slice
+    edges, in one slice or in the row tail, and speculating lists that must
+    rescan.  Exact against the oracle."""
+    monkeypatch.setenv("FG_HIP_TARGET_GROUPS", str(groups))
+    monkeypatch.setenv("FG_HIP_FRONT_SHARE", str(share))
+    monkeypatch.setenv("FG_HIP_PAIRED", "1")  # row 7's penalties would keep row-major halves
+    rng = np.random.default_rng(groups + share + k)
+    rows, vocab = 16, W.V
+    logits = rng.normal(0, 1, (rows, vocab)).astype(np.float32)
+    logits[0, :600] = 50 + rng.normal(0, 1, 600)                  # top values at the row start
+    logits[1] = np.linspace(-5, 5, vocab, dtype=np.float32)        # ascending
+    logits[2, 75_000:80_000] = 20 + rng.normal(0, 1, 5000)         # across the halves' boundary
+    logits[3, 151_000:] = 40 + rng.normal(0, 1, vocab - 151_000)   # the row tail
+    logits[4, :] = 1.0                                             # tied, a few higher
+    logits[4, 98_000:98_100] = 2.0
+    for r in (5, 6):                                               # one value per 4096 block
+        logits[r, ::4096] = 10 + rng.normal(0, 0.1, len(range(0, vocab, 4096)))
+    counts = np.zeros((rows, vocab), dtype=np.uint32)
+    counts[7, :300] = rng.integers(1, 5, 300)
+    logits[7, :300] = 60.0
+    configs = [W.cfg(0.8, 0.9 if k else 0.3, k, presence=0.4 if r == 7 else 0.0)
+               for r in range(rows)]
+    w = dict(logits=logits, counts=counts, configs=configs,
+             uniforms=rng.random(rows).astype(np.float32), logprobs=0)
+    if k:
+        check(w, run_hip(w, dev), W.oracle_run(w), f"paired groups={groups} share={share} k={k}")
+    else:
+        check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), W.oracle_run(w),
+              f"paired nucleus groups={groups} share={share}", NUC_BOUNDARY)
