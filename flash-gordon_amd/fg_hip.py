@@ -429,4 +429,7 @@ class HipSampler:
 
 def env_summary() -> dict:
     return {"lib": str(LIB_PATH), "exists": LIB_PATH.exists(),
-            "target_groups": os.environ.get("FG_HIP_TARGET_GROUPS")}
+            "target_groups": os.environ.get("FG_HIP_TARGET_GROUPS"),
+            "paired": os.environ.get("FG_HIP_PAIRED"),
+            "front_share": os.environ.get("FG_HIP_FRONT_SHARE"),
+            "pace": os.environ.get("FG_HIP_PACE")}
