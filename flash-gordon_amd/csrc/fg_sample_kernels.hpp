@@ -54,6 +54,7 @@ constexpr uint32_t kSpecMinK = 32;   // top lists longer than this stage specula
 constexpr uint32_t kSpecMaxSteps = 24;  // ... over wave slices of at most this many steps
 constexpr uint32_t kMaxChunks = 64;  // workgroups per row
 constexpr uint32_t kDefaultGroups = 512;   // chunking: ceil(512 / rows) chunks per row
+constexpr uint32_t kNucleusGroups = 768;   // chunking with whole-row nucleus rows
 constexpr uint32_t kMaxGroups = 1024;      // workspace: workgroups a launch may use beyond rows
 constexpr uint32_t kLineWords = 32;  // u32 per 128-byte cache line (row counters)
 

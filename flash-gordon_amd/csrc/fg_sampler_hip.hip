@@ -533,14 +533,22 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
     return arg_fail(err, "invalid sampled output arguments");
   const uint32_t vocab = s->vocab;
   // Chunking (measured on MI355X, V = 151,936): ceil(512 / rows) chunks,
-  // two workgroups per CU (config 2's 64 rows: 8 chunks; config 3's 256: 2;
-  // config 4's 128 rows: 4 chunks 28.1 us against 8 chunks 29.9-31.1; one
-  // row: 64).  FG_HIP_TARGET_GROUPS overrides: ceil(target / rows) chunks.
-  // At most kMaxChunks per row; each wave slice a multiple of 4 elements.
+  // two workgroups per CU (config 2's 64 rows: 8 chunks, 21.5 us against
+  // 25.2 at 12; config 4's 128 rows: 4 chunks, 28.0 us against 29.2 at 6 and
+  // 29.9-31.1 at 8; one row: 64).  Launches with whole-row nucleus rows (an
+  // exp per element) take ceil(768 / rows), three per CU (config 3's 256
+  // rows: 3 chunks 69.1 us against 72.7 at 2 and 85.6 at 4).
+  // FG_HIP_TARGET_GROUPS overrides: ceil(target / rows) chunks.  At most
+  // kMaxChunks per row; each wave slice a multiple of 4 elements.
   bool same_cost = true;  // every row alike in penalties (for the paired layout)
-  for (uint32_t r = 1; r < b->rows; r++)
+  bool nuc_rows = false;
+  for (uint32_t r = 0; r < b->rows; r++) {
     same_cost &= ((s->h_params[r].flags ^ s->h_params[0].flags) & fg::kRowPenalties) == 0u;
-  const uint32_t target = s->target_groups ? s->target_groups : fg::kDefaultGroups;
+    nuc_rows |= s->h_params[r].temperature > 0.0f && s->h_params[r].top_k == 0u;
+  }
+  const uint32_t target = s->target_groups ? s->target_groups
+                          : nuc_rows       ? fg::kNucleusGroups
+                                           : fg::kDefaultGroups;
   uint32_t chunks = (target + b->rows - 1u) / b->rows;
   if (chunks > fg::kMaxChunks) chunks = fg::kMaxChunks;
   if (chunks < 1u) chunks = 1u;
