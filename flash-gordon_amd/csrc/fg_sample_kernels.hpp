@@ -783,14 +783,54 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
 
 // Wave slice i of a row (i = chunk * kWaves + wave): [begin, begin + len)
 // clipped to the vocabulary.
+__host__ __device__ inline uint32_t slice_begin_of(uint32_t i, uint32_t split, uint32_t ea,
+                                                   uint32_t eb, uint32_t vocab) {
+  const uint32_t na = split * kWaves;
+  const uint32_t b = i < na ? i * ea : na * ea + (i - na) * eb;
+  return b < vocab ? b : vocab;
+}
+__host__ __device__ inline uint32_t slice_end_of(uint32_t i, uint32_t split, uint32_t ea,
+                                                 uint32_t eb, uint32_t vocab) {
+  const uint32_t e = slice_begin_of(i, split, ea, eb, vocab) + (i < split * kWaves ? ea : eb);
+  return e < vocab ? e : vocab;
+}
 __device__ __forceinline__ uint32_t slice_begin(const SampleArgs& a, uint32_t i) {
-  const uint32_t na = a.split * kWaves;
-  const uint32_t b = i < na ? i * a.wave_elems : na * a.wave_elems + (i - na) * a.wave_elems_b;
-  return min(b, a.vocab);
+  return slice_begin_of(i, a.split, a.wave_elems, a.wave_elems_b, a.vocab);
 }
 __device__ __forceinline__ uint32_t slice_end(const SampleArgs& a, uint32_t i) {
-  const uint32_t len = i < a.split * kWaves ? a.wave_elems : a.wave_elems_b;
-  return min(slice_begin(a, i) + len, a.vocab);
+  return slice_end_of(i, a.split, a.wave_elems, a.wave_elems_b, a.vocab);
+}
+
+// The row and chunk of workgroup b.  A row's chunks share one XCD (and its
+// L2): the dispatcher hands workgroups to the kXcds XCDs round robin, so row
+// r's chunks take blockIdx values of residue r % kXcds.  With split < chunks
+// (rows a multiple of kXcds, two equal halves of chunks) chunks [0, split)
+// sit in the grid's first half and the rest in its second: the
+// first-dispatched workgroup of a CU streams faster than the second.  Rows
+// past the last whole group of kXcds are laid out row-major after them.
+// Only speed depends on the dispatch order; any order is correct.
+__host__ __device__ inline void block_row_chunk(uint32_t b, uint32_t rows, uint32_t chunks,
+                                                uint32_t split, uint32_t* row, uint32_t* chunk) {
+  const uint32_t grouped = rows - rows % kXcds;
+  if (split < chunks) {
+    const uint32_t half = rows * split;  // workgroups per half
+    const bool second = b >= half;
+    const uint32_t bb = second ? b - half : b;
+    const uint32_t hc = second ? chunks - split : split;
+    const uint32_t q = bb / kXcds;
+    const uint32_t g = q / hc;
+    *row = g * kXcds + bb % kXcds;
+    *chunk = q - g * hc + (second ? split : 0u);
+  } else if (b < grouped * chunks) {
+    const uint32_t q = b / kXcds;
+    const uint32_t g = q / chunks;
+    *row = g * kXcds + b % kXcds;
+    *chunk = q - g * chunks;
+  } else {
+    const uint32_t r = (b - grouped * chunks) / chunks;
+    *row = grouped + r;
+    *chunk = b - grouped * chunks - r * chunks;
+  }
 }
 
 // Reads wave slice `i` of the row again and merges into `fin` (the row's list)
@@ -893,38 +933,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   // waterfall loop).
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t lane = lane_id();
-  // A row's chunks share one XCD (and its L2): the dispatcher hands
-  // workgroups to the kXcds XCDs round robin, so row r's chunks take blockIdx
-  // values of residue r % kXcds.  With split < chunks (rows a multiple of
-  // kXcds, two halves of chunks) chunks [0, split) sit in the grid's first
-  // half and the rest in its second: the first-dispatched workgroup of a CU
-  // streams faster than the second, so its slices are made longer.  Rows past
-  // the last whole group of kXcds are laid out row-major after them.  Only
-  // speed depends on the dispatch order; any order is correct.
   uint32_t row, chunk;
-  {
-    const uint32_t b = blockIdx.x;
-    const uint32_t grouped = a.rows - a.rows % kXcds;
-    if (a.split < a.chunks) {
-      const uint32_t half = a.rows * a.split;  // workgroups per half
-      const bool second = b >= half;
-      const uint32_t bb = second ? b - half : b;
-      const uint32_t hc = second ? a.chunks - a.split : a.split;
-      const uint32_t q = bb / kXcds;
-      const uint32_t g = q / hc;
-      row = g * kXcds + bb % kXcds;
-      chunk = q - g * hc + (second ? a.split : 0u);
-    } else if (b < grouped * a.chunks) {
-      const uint32_t q = b / kXcds;
-      const uint32_t g = q / a.chunks;
-      row = g * kXcds + b % kXcds;
-      chunk = q - g * a.chunks;
-    } else {
-      const uint32_t r = (b - grouped * a.chunks) / a.chunks;
-      row = grouped + r;
-      chunk = b - grouped * a.chunks - r * a.chunks;
-    }
-  }
+  block_row_chunk(blockIdx.x, a.rows, a.chunks, a.split, &row, &chunk);
   const RowParams p = a.params[row];
   const float urow = a.uniforms[row];  // early: the row's last step needs it
   const bool greedy = p.temperature == 0.0f;

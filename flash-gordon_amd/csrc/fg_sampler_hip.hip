@@ -134,6 +134,87 @@ constexpr uint32_t kPairedMaxGroups = 512u;
 constexpr uint32_t kFrontPermilleTwo = 580u;
 constexpr uint32_t kFrontPermilleMany = 500u;
 
+namespace {
+
+// Launch-geometry overrides read from the environment (0 / -1: the rule).
+struct Tuning {
+  uint32_t target_groups = 0u;   // FG_HIP_TARGET_GROUPS
+  uint32_t front_permille = 0u;  // FG_HIP_FRONT_SHARE (500..749)
+  int32_t paired = -1;           // FG_HIP_PAIRED (0 / 1)
+  int32_t pace = -1;             // FG_HIP_PACE (0 / 1)
+};
+Tuning tuning_from_env() {
+  Tuning t;
+  if (const char* v = getenv("FG_HIP_TARGET_GROUPS")) {
+    const long x = strtol(v, nullptr, 10);
+    if (x >= 1 && x <= 1 << 20) t.target_groups = static_cast<uint32_t>(x);
+  }
+  if (const char* v = getenv("FG_HIP_FRONT_SHARE")) {
+    const long x = strtol(v, nullptr, 10);
+    if (x >= 500 && x < 750) t.front_permille = static_cast<uint32_t>(x);
+  }
+  if (const char* v = getenv("FG_HIP_PAIRED")) t.paired = atoi(v) != 0;
+  if (const char* v = getenv("FG_HIP_PACE")) t.pace = atoi(v) != 0;
+  return t;
+}
+
+// Launch geometry of a batch (see fg_sampler_hip_geometry).
+//
+// Chunking (measured on MI355X, V = 151,936): ceil(512 / rows) chunks, two
+// workgroups per CU (config 2's 64 rows: 8 chunks, 21.5 us against 25.2 at
+// 12; config 4's 128 rows: 4 chunks, 28.0 us against 29.2 at 6 and 29.9-31.1
+// at 8; one row: 64).  Launches with whole-row nucleus rows (an exp per
+// element) take ceil(768 / rows), three per CU (config 3's 256 rows: 3
+// chunks 69.1 us against 72.7 at 2 and 85.6 at 4).  At most kMaxChunks per
+// row; each wave slice a multiple of 4 elements.
+//
+// Layout: the first workgroup dispatched to a CU streams faster than the
+// second (measured: ~8% at 8 chunks of V = 151,936 per row, ~12% at 2).
+// With the rows a multiple of the XCD count, an even chunk count, at most
+// two workgroups per CU and rows of like cost, a row's first chunks go to
+// the grid's first half (longer slices at two chunks per row), the others
+// to its second half.  Rows of unlike cost keep the row-major halves: the
+// costlier rows (first in the batch) then run in the faster first half
+// (config 4, penalties on rows 0-63 only: 28.1 us against 30.2 paired).
+void plan_geometry(uint32_t vocab, uint32_t rows, bool nuc_rows, bool same_cost, const Tuning& t,
+                   fg_sampler_hip_geometry* g) {
+  const uint32_t target = t.target_groups ? t.target_groups
+                          : nuc_rows      ? fg::kNucleusGroups
+                                          : fg::kDefaultGroups;
+  uint32_t chunks = (target + rows - 1u) / rows;
+  if (chunks > fg::kMaxChunks) chunks = fg::kMaxChunks;
+  if (chunks < 1u) chunks = 1u;
+  const uint32_t waves = chunks * fg::kWaves;
+  uint32_t wave_elems = (vocab + waves - 1u) / waves;
+  wave_elems = (wave_elems + 3u) & ~3u;
+  if (wave_elems < 4u) wave_elems = 4u;
+  chunks = (vocab + wave_elems * fg::kWaves - 1u) / (wave_elems * fg::kWaves);
+  g->chunks = chunks;
+  g->split = chunks;
+  g->wave_elems = wave_elems;
+  g->wave_elems_b = wave_elems;
+  g->pace = t.pace >= 0 ? static_cast<uint32_t>(t.pace) : 1u;
+  const bool paired_rule =
+      same_cost && static_cast<uint64_t>(rows) * chunks <= kPairedMaxGroups;
+  if (rows % fg::kXcds == 0u && chunks % 2u == 0u && (t.paired >= 0 ? t.paired != 0 : paired_rule)) {
+    const uint32_t permille = t.front_permille ? t.front_permille
+                              : chunks == 2u   ? kFrontPermilleTwo
+                                               : kFrontPermilleMany;
+    const uint32_t na = chunks / 2u * fg::kWaves;
+    uint64_t ea = (static_cast<uint64_t>(vocab) * permille + 1000u * na - 1u) / (1000u * na);
+    ea = (ea + 3u) & ~3ull;
+    if (ea * na < vocab) {
+      uint64_t eb = (vocab - ea * na + na - 1u) / na;
+      eb = (eb + 3u) & ~3ull;
+      g->wave_elems = static_cast<uint32_t>(ea);
+      g->wave_elems_b = static_cast<uint32_t>(eb);
+      g->split = chunks / 2u;
+    }
+  }
+}
+
+}  // namespace
+
 struct fg_sampler_hip {
   int device;
   uint32_t vocab;
@@ -150,10 +231,7 @@ struct fg_sampler_hip {
   uint32_t* d_row_done;     // [max_rows * kLineWords]
   uint32_t* d_nuc_deep;     // [max_rows]
   float* d_nuc_max;         // [max_rows]
-  uint32_t target_groups;   // FG_HIP_TARGET_GROUPS, 0 = the built-in chunking rule
-  uint32_t front_permille;  // FG_HIP_FRONT_SHARE: first-half share override, 0 = the rule
-  int32_t paired_override;  // FG_HIP_PAIRED: 0 / 1 forces the layout, -1 = the rule
-  int32_t pace_override;    // FG_HIP_PACE: 0 / 1 forces priority pacing, -1 = the rule
+  Tuning tuning;            // environment overrides, read at create
   uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
   uint64_t* counters;       // event counters, FG_SAMPLE_TRACE builds only
 };
@@ -421,24 +499,12 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   }
   s->vocab = vocab;
   s->max_rows = max_rows;
-  s->target_groups = 0u;  // 0: the built-in chunking rule
-  if (const char* t = getenv("FG_HIP_TARGET_GROUPS")) {
-    const long v = strtol(t, nullptr, 10);
-    if (v >= 1 && v <= 1 << 20) s->target_groups = static_cast<uint32_t>(v);
-  }
-  s->front_permille = 0u;
-  s->paired_override = -1;
-  s->pace_override = -1;
-  if (const char* t = getenv("FG_HIP_PAIRED")) s->paired_override = atoi(t) != 0;
-  if (const char* t = getenv("FG_HIP_PACE")) s->pace_override = atoi(t) != 0;
-  if (const char* t = getenv("FG_HIP_FRONT_SHARE")) {
-    const long v = strtol(t, nullptr, 10);
-    if (v >= 500 && v < 750) s->front_permille = static_cast<uint32_t>(v);
-  }
+  s->tuning = tuning_from_env();
   hipError_t e = hipGetDevice(&s->device);
   // rows * chunks(rows) <= max(target, kMaxGroups) + rows for every batch
   // size.
-  const uint64_t groups_cap = s->target_groups > fg::kMaxGroups ? s->target_groups : fg::kMaxGroups;
+  const uint64_t groups_cap =
+      s->tuning.target_groups > fg::kMaxGroups ? s->tuning.target_groups : fg::kMaxGroups;
   const uint64_t slots = (groups_cap + max_rows) * fg::kWaves;
   s->slots = slots;
   s->h_params = static_cast<RowParams*>(calloc(max_rows, sizeof(RowParams)));
@@ -532,32 +598,15 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
       (b->logprobs && (!b->logprob_values || !b->logprob_ids)))
     return arg_fail(err, "invalid sampled output arguments");
   const uint32_t vocab = s->vocab;
-  // Chunking (measured on MI355X, V = 151,936): ceil(512 / rows) chunks,
-  // two workgroups per CU (config 2's 64 rows: 8 chunks, 21.5 us against
-  // 25.2 at 12; config 4's 128 rows: 4 chunks, 28.0 us against 29.2 at 6 and
-  // 29.9-31.1 at 8; one row: 64).  Launches with whole-row nucleus rows (an
-  // exp per element) take ceil(768 / rows), three per CU (config 3's 256
-  // rows: 3 chunks 69.1 us against 72.7 at 2 and 85.6 at 4).
-  // FG_HIP_TARGET_GROUPS overrides: ceil(target / rows) chunks.  At most
-  // kMaxChunks per row; each wave slice a multiple of 4 elements.
   bool same_cost = true;  // every row alike in penalties (for the paired layout)
   bool nuc_rows = false;
   for (uint32_t r = 0; r < b->rows; r++) {
     same_cost &= ((s->h_params[r].flags ^ s->h_params[0].flags) & fg::kRowPenalties) == 0u;
     nuc_rows |= s->h_params[r].temperature > 0.0f && s->h_params[r].top_k == 0u;
   }
-  const uint32_t target = s->target_groups ? s->target_groups
-                          : nuc_rows       ? fg::kNucleusGroups
-                                           : fg::kDefaultGroups;
-  uint32_t chunks = (target + b->rows - 1u) / b->rows;
-  if (chunks > fg::kMaxChunks) chunks = fg::kMaxChunks;
-  if (chunks < 1u) chunks = 1u;
-  const uint32_t waves = chunks * fg::kWaves;
-  uint32_t wave_elems = (vocab + waves - 1u) / waves;
-  wave_elems = (wave_elems + 3u) & ~3u;
-  if (wave_elems < 4u) wave_elems = 4u;
-  chunks = (vocab + wave_elems * fg::kWaves - 1u) / (wave_elems * fg::kWaves);
-
+  fg_sampler_hip_geometry geo;
+  plan_geometry(vocab, b->rows, nuc_rows, same_cost, s->tuning, &geo);
+  const uint32_t chunks = geo.chunks;
   if (static_cast<uint64_t>(b->rows) * chunks * fg::kWaves > s->slots) {
     fg_error_set(err, FG_ERR_LIMIT, "sampler workspace too small for %u rows", b->rows);
     return FG_ERR_LIMIT;
@@ -572,36 +621,10 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
   a.vocab = vocab;
   a.rows = b->rows;
   a.chunks = chunks;
-  a.wave_elems = wave_elems;
-  a.wave_elems_b = wave_elems;
-  a.split = chunks;
-  // The first workgroup dispatched to a CU streams faster than the second
-  // (measured: ~8% at 8 chunks of V = 151,936 per row, ~12% at 2).  With
-  // the rows a multiple of the XCD count, an even chunk count and at most
-  // two workgroups per CU, a row's first chunks go to the grid's first half
-  // (longer slices at two chunks per row), the others to its second half.
-  a.pace = s->pace_override >= 0 ? static_cast<uint32_t>(s->pace_override) : 1u;
-  // Rows of unlike cost keep the row-major halves: the costlier rows (first
-  // in the batch) then run in the faster first half (config 4, penalties on
-  // rows 0-63 only: 28.1 us against 30.2 paired).
-  const bool paired_rule =
-      same_cost && static_cast<uint64_t>(b->rows) * chunks <= kPairedMaxGroups;
-  if (b->rows % fg::kXcds == 0u && chunks % 2u == 0u &&
-      (s->paired_override >= 0 ? s->paired_override != 0 : paired_rule)) {
-    const uint32_t permille = s->front_permille ? s->front_permille
-                              : chunks == 2u    ? kFrontPermilleTwo
-                                                : kFrontPermilleMany;
-    const uint32_t na = chunks / 2u * fg::kWaves;
-    uint64_t ea = (static_cast<uint64_t>(vocab) * permille + 1000u * na - 1u) / (1000u * na);
-    ea = (ea + 3u) & ~3ull;
-    if (ea * na < vocab) {
-      uint64_t eb = (vocab - ea * na + na - 1u) / na;
-      eb = (eb + 3u) & ~3ull;
-      a.wave_elems = static_cast<uint32_t>(ea);
-      a.wave_elems_b = static_cast<uint32_t>(eb);
-      a.split = chunks / 2u;
-    }
-  }
+  a.wave_elems = geo.wave_elems;
+  a.wave_elems_b = geo.wave_elems_b;
+  a.split = geo.split;
+  a.pace = geo.pace;
   a.logprobs = b->logprobs;
   a.tokens = b->tokens;
   a.token_logits = b->token_logits;
@@ -676,3 +699,28 @@ fg_status fg_sampler_hip_trace_counters(fg_sampler_hip* s, uint64_t* host) {
 #endif
 
 }  // extern "C"
+
+extern "C" fg_status fg_sampler_hip_plan(uint32_t vocab, uint32_t rows, uint32_t traits,
+                                         fg_sampler_hip_geometry* out, fg_error* err) {
+  if (!out || !vocab || vocab >= 0x80000000u || !rows || (traits & ~3u))
+    return arg_fail(err, "invalid geometry arguments");
+  plan_geometry(vocab, rows, (traits & FG_SAMPLER_HIP_ROWS_NUCLEUS) != 0u,
+                (traits & FG_SAMPLER_HIP_ROWS_UNLIKE_COST) == 0u, tuning_from_env(), out);
+  return FG_OK;
+}
+
+extern "C" fg_status fg_sampler_hip_block(const fg_sampler_hip_geometry* g, uint32_t vocab,
+                                          uint32_t rows, uint32_t block, uint32_t wave,
+                                          uint32_t* row, uint32_t* chunk, uint32_t* begin,
+                                          uint32_t* end, fg_error* err) {
+  if (!g || !row || !chunk || !begin || !end || !vocab || !rows || !g->chunks ||
+      g->split > g->chunks || (g->split < g->chunks && (rows % fg::kXcds || 2u * g->split != g->chunks)) ||
+      static_cast<uint64_t>(block) >= static_cast<uint64_t>(rows) * g->chunks ||
+      wave >= static_cast<uint32_t>(fg::kWaves))
+    return arg_fail(err, "invalid block arguments");
+  fg::block_row_chunk(block, rows, g->chunks, g->split, row, chunk);
+  const uint32_t i = *chunk * fg::kWaves + wave;
+  *begin = fg::slice_begin_of(i, g->split, g->wave_elems, g->wave_elems_b, vocab);
+  *end = fg::slice_end_of(i, g->split, g->wave_elems, g->wave_elems_b, vocab);
+  return FG_OK;
+}

@@ -48,11 +48,21 @@ EXPORTS = (
     "fg_f16_to_f32", "fg_f32_to_f16", "fg_quantize_q8_0", "fg_dequantize_q8_0",
     "fg_q8_0_cooked_tile_bytes", "fg_q8_0_cooked_matrix_bytes", "fg_cook_q8_0_rows",
     "fg_uncook_q8_0_rows", "fg_hip_dense_q8_0_cooked", "fg_hip_output_slice_run_dense",
+    "fg_sampler_hip_plan", "fg_sampler_hip_block",
 )
+
+ROWS_NUCLEUS = 1
+ROWS_UNLIKE_COST = 2
 
 
 class FgError(C.Structure):
     _fields_ = [("code", C.c_int), ("message", C.c_char * 512)]
+
+
+class Geometry(C.Structure):
+    """fg_sampler_hip_geometry (include/fg_sampler_hip.h)."""
+    _fields_ = [("chunks", C.c_uint32), ("split", C.c_uint32), ("wave_elems", C.c_uint32),
+                ("wave_elems_b", C.c_uint32), ("pace", C.c_uint32)]
 
 
 class SamplerConfig(C.Structure):
@@ -155,6 +165,10 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_hip_dense_q8_0_cooked": (C.c_int, [P, P, P, u32, u32, u32, f32, P, E]),
         "fg_hip_output_slice_run_dense":
             (C.c_int, [P, P, P, u32, u32, f32, P, P, P, P, P, E]),
+        "fg_sampler_hip_plan": (C.c_int, [u32, u32, u32, C.POINTER(Geometry), E]),
+        "fg_sampler_hip_block": (C.c_int, [C.POINTER(Geometry), u32, u32, u32, u32,
+                                           C.POINTER(u32), C.POINTER(u32), C.POINTER(u32),
+                                           C.POINTER(u32), E]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -425,6 +439,22 @@ class HipSampler:
         _check(self._lib.fg_sampler_hip_history_increment(
             self.handle, _ptr(counts), counts.stride(0), _ptr(tokens), _ptr(row_status), rows,
             _stream(stream), C.byref(err)), err)
+
+
+def plan(vocab: int, rows: int, traits: int = 0) -> Geometry:
+    """Launch geometry of fg_sampler_hip_sample (host only, no device)."""
+    g, err = Geometry(), FgError()
+    _check(lib().fg_sampler_hip_plan(vocab, rows, traits, C.byref(g), C.byref(err)), err)
+    return g
+
+
+def block(g: Geometry, vocab: int, rows: int, b: int, wave: int):
+    """(row, chunk, begin, end) of wave `wave` of workgroup `b` (host only)."""
+    out = [C.c_uint32() for _ in range(4)]
+    err = FgError()
+    _check(lib().fg_sampler_hip_block(C.byref(g), vocab, rows, b, wave,
+                                      *[C.byref(o) for o in out], C.byref(err)), err)
+    return tuple(o.value for o in out)
 
 
 def env_summary() -> dict:

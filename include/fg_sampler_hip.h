@@ -180,6 +180,36 @@ typedef struct fg_sampler_hip_batch {
 fg_status fg_sampler_hip_sample(fg_sampler_hip *sampler, const fg_sampler_hip_batch *batch,
                                 void *stream, fg_error *err);
 
+/* Launch geometry of fg_sampler_hip_sample, for tests and tuning (no
+ * counterpart in the reference, whose per-tile dispatches have a fixed
+ * shape, shaders/fg_topk_select.comp).  Each row is split into `chunks`
+ * workgroups of four waves; wave i = chunk * 4 + w streams elements
+ * [begin, end) of its row, slices of `wave_elems` for chunks < split and
+ * `wave_elems_b` after.  split < chunks: the row's chunks are divided between
+ * the grid's two dispatch halves. */
+typedef struct fg_sampler_hip_geometry {
+    uint32_t chunks;
+    uint32_t split;
+    uint32_t wave_elems;
+    uint32_t wave_elems_b;
+    uint32_t pace; /* 1: waves step their issue priority down as they progress */
+} fg_sampler_hip_geometry;
+
+#define FG_SAMPLER_HIP_ROWS_NUCLEUS 1u     /* some row is a whole-row nucleus (top_k 0) */
+#define FG_SAMPLER_HIP_ROWS_UNLIKE_COST 2u /* rows differ in whether penalties apply */
+
+/* The geometry a sampler created now (same environment) uses for `rows` rows
+ * of `vocab` logits with the given FG_SAMPLER_HIP_ROWS_* traits.  Host only:
+ * no device is needed.  FG_ERR_ARGUMENT on invalid arguments. */
+fg_status fg_sampler_hip_plan(uint32_t vocab, uint32_t rows, uint32_t traits,
+                              fg_sampler_hip_geometry *out, fg_error *err);
+
+/* Which row and chunk workgroup `block` of such a launch takes, and the
+ * element range [begin, end) of its wave `wave` (0-3).  Host only. */
+fg_status fg_sampler_hip_block(const fg_sampler_hip_geometry *g, uint32_t vocab, uint32_t rows,
+                               uint32_t block, uint32_t wave, uint32_t *row, uint32_t *chunk,
+                               uint32_t *begin, uint32_t *end, fg_error *err);
+
 /* After a draw, adds 1 (saturating) to counts[r*stride + tokens[r]] for every
  * row whose config has penalties active and whose row_status is FG_OK (or
  * row_status == NULL).  Replaces fg_output_history_increment as called at
