@@ -43,15 +43,14 @@ constexpr uint32_t kRowPenalties = 1u;
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr int kStepVec = 4;  // quads (4 elements) per lane per streaming step
-constexpr uint32_t kStepQuads = kWave * kStepVec;
-constexpr uint32_t kStepElems = kStepQuads * 4u;
+constexpr int kMaxStepVec = 4;  // quads (4 elements) per lane per streaming step, at most
+constexpr uint32_t kStepElems = kWave * kMaxStepVec * 4u;  // elements per step, at most
 // LDS staging per wave: fewer than 64 left over plus one full step.
 constexpr uint32_t kCap = 64u + kStepElems;
 constexpr uint32_t kMaxK = 64;       // largest top-k / log-prob count
 constexpr uint32_t kXcds = 8;  // XCDs of an MI355X (workgroups go round robin)
 constexpr uint32_t kSpecMinK = 32;   // top lists longer than this stage speculatively
-constexpr uint32_t kSpecMaxSteps = 24;  // ... over wave slices of at most this many steps
+constexpr uint32_t kSpecMaxElems = 24u * 1024u;  // ... over wave slices of at most this many steps
 constexpr uint32_t kMaxChunks = 64;  // workgroups per row
 constexpr uint32_t kDefaultGroups = 512;   // chunking: ceil(512 / rows) chunks per row
 constexpr uint32_t kNucleusGroups = 768;   // chunking with whole-row nucleus rows
@@ -526,6 +525,11 @@ struct Features {
   static constexpr bool kLse = kLse_;      // log-probs requested
   static constexpr bool kNuc = kNuc_;      // some row is a whole-row nucleus (top_k 0)
   static constexpr bool kSpec = kSpec_;    // some top list is longer than kSpecMinK
+  // Quads per lane per streaming step: 2 (512 elements) for launches
+  // without speculation or whole-row nucleus rows, 4 otherwise (measured:
+  // config 2 21.9 -> 21.1 us at 512, config 4 greedy 22.4 -> 21.8; top-k 64
+  // 23.1 -> 23.6 and config 3 79 -> 85 would lose).
+  static constexpr int kStepVec = (kSpec_ || kNuc_) ? 4 : 2;
 };
 
 template <bool kVec>
@@ -603,7 +607,7 @@ __device__ __forceinline__ uint64_t greedy_lane_comp(const WaveState& st) {
   return st.gid != kInvalidId ? greedy_comp(st.gv, st.gid) : 0ull;
 }
 
-// One streaming step: x/y hold quads q0 + j*64 + lane (j < kStepVec); quads
+// One streaming step: x/y hold quads q0 + j*64 + lane (j < F::kStepVec); quads
 // at or past q_end are clamped duplicates and are masked out.
 template <class F>
 __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, bool pen,
@@ -612,10 +616,10 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
                                              float* prow, const f4* x, const u4* y, uint32_t q0,
                                              uint32_t q_end) {
   const uint32_t lane = lane_id();
-  float v[kStepVec][4];
-  bool ok[kStepVec];
+  float v[F::kStepVec][4];
+  bool ok[F::kStepVec];
 #pragma unroll
-  for (int j = 0; j < kStepVec; j++) {
+  for (int j = 0; j < F::kStepVec; j++) {
     const uint32_t q = q0 + j * kWave + lane;
     ok[j] = q < q_end;
     v[j][0] = x[j].x;
@@ -628,7 +632,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
     // slot pays for the IEEE division only when one of its lanes needs it,
     // and then without branches.
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++) {
+    for (int j = 0; j < F::kStepVec; j++) {
       const uint32_t c4[4] = {y[j].x, y[j].y, y[j].z, y[j].w};
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -639,7 +643,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
   }
   if (prow) {
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++)
+    for (int j = 0; j < F::kStepVec; j++)
       if (ok[j]) {
         const uint32_t q = q0 + j * kWave + lane;
 #pragma unroll
@@ -648,7 +652,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
   }
   if (F::kGreedy && greedy) {
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++) {
+    for (int j = 0; j < F::kStepVec; j++) {
       const uint32_t q = q0 + j * kWave + lane;
 #pragma unroll
       for (int e = 0; e < 4; e++) greedy_stream(st, ok[j], v[j][e], q * 4u + e);
@@ -657,7 +661,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
   if (F::kLse && lse) {
     float step_max = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++)
+    for (int j = 0; j < F::kStepVec; j++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
         if (ok[j] && is_finite_bits(__float_as_uint(v[j][e]))) step_max = fmaxf(step_max, v[j][e]);
@@ -666,7 +670,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
       st.lm = step_max;
     }
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++)
+    for (int j = 0; j < F::kStepVec; j++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
         if (ok[j] && is_finite_bits(__float_as_uint(v[j][e])))
@@ -675,7 +679,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
   if (F::kNuc && nuc) {
     float step_max = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++)
+    for (int j = 0; j < F::kStepVec; j++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
         if (ok[j] && is_finite_bits(__float_as_uint(v[j][e]))) step_max = fmaxf(step_max, v[j][e]);
@@ -692,10 +696,10 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
     }
     // The step's f32 terms summed pairwise in f32 (four roundings), then in
     // f64; their error bound sum w * (max - s) in f32.
-    float w[kStepVec * 4];
+    float w[F::kStepVec * 4];
     float ef = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++)
+    for (int j = 0; j < F::kStepVec; j++)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const bool use = ok[j] && is_finite_bits(__float_as_uint(v[j][e]));
@@ -704,7 +708,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
         ef = fmaf(w[j * 4 + e], -sd, ef);
       }
 #pragma unroll
-    for (int h = kStepVec * 2; h >= 1; h /= 2)
+    for (int h = F::kStepVec * 2; h >= 1; h /= 2)
 #pragma unroll
       for (int i = 0; i < h; i++) w[i] = w[i] + w[i + h];
     st.nz += static_cast<double>(w[0]);
@@ -715,7 +719,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
     // drained); NaN does not.
     float lane_max = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kStepVec; j++) {
+    for (int j = 0; j < F::kStepVec; j++) {
       const float m = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
       lane_max = ok[j] ? fmaxf(lane_max, m) : lane_max;
     }
@@ -727,7 +731,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
       if (ballot(lane_max == INFINITY) != 0ull) {
         lane_max_key = 0u;
 #pragma unroll
-        for (int j = 0; j < kStepVec; j++)
+        for (int j = 0; j < F::kStepVec; j++)
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             const uint32_t key = ok[j] ? float_key(v[j][e]) : 0u;
@@ -768,7 +772,7 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
     if (ballot(lane_max >= f) != 0ull) {
       FG_COUNT(2, 1ull);
 #pragma unroll
-      for (int j = 0; j < kStepVec; j++) {
+      for (int j = 0; j < F::kStepVec; j++) {
         const uint32_t q = q0 + j * kWave + lane;
         const float fj = ok[j] ? f : __builtin_nanf("");
 #pragma unroll
@@ -949,7 +953,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   // slices the exact filter soon passes it, and a check that fails would
   // read a long slice again.
   const bool spec = F::kSpec && !greedy && kk > kSpecMinK &&
-                    max(a.wave_elems, a.wave_elems_b) <= kSpecMaxSteps * kStepElems;
+                    max(a.wave_elems, a.wave_elems_b) <= kSpecMaxElems;
   const float t_eff = p.temperature > 0.0f ? p.temperature : 1.0f;
   const float log2e_over_t = 1.4426950408889634f / t_eff;
   // 1 / T for the finish, divided here where the loads' latency hides it.
@@ -978,16 +982,16 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     // Double-buffered, the two buffers taking turns (no register copies,
     // which would wait for the loads on the back edge): step s+1 is loaded
     // before step s is processed.  (Loading further ahead measured slower.)
-    f4 xa[kStepVec], xb[kStepVec];
-    u4 ya[kStepVec], yb[kStepVec];
+    f4 xa[F::kStepVec], xb[F::kStepVec];
+    u4 ya[F::kStepVec], yb[F::kStepVec];
     const bool cnt = F::kPen && pen;
     const uint32_t slice_bytes = (q_end - q_begin) * 16u;
     const __amdgpu_buffer_rsrc_t rl = slice_rsrc(lrow + 4u * q_begin, slice_bytes);
     const __amdgpu_buffer_rsrc_t rc =
         slice_rsrc(cnt ? static_cast<const void*>(crow + 4u * q_begin) : lrow, cnt ? slice_bytes : 0u);
-    auto load = [&](f4 (&x)[kStepVec], u4 (&y)[kStepVec], uint32_t qs) {
+    auto load = [&](f4 (&x)[F::kStepVec], u4 (&y)[F::kStepVec], uint32_t qs) {
 #pragma unroll
-      for (int j = 0; j < kStepVec; j++) {
+      for (int j = 0; j < F::kStepVec; j++) {
         if constexpr (F::kVec)
           load_quad_buf(rl, rc, cnt, qs - q_begin + j * kWave + lane, x[j], y[j]);
         else
@@ -1013,13 +1017,13 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       }
     };
     for (uint32_t q0 = q_begin;;) {
-      load(xb, yb, q0 + kStepQuads);
+      load(xb, yb, q0 + (kWave * F::kStepVec));
       process_step<F>(st, p, pen, greedy, lse, nuc, spec, log2e_over_t, prow, xa, ya, q0, q_end);
-      if ((q0 += kStepQuads) >= q_end) break;
+      if ((q0 += (kWave * F::kStepVec)) >= q_end) break;
       pace(q0);
-      load(xa, ya, q0 + kStepQuads);
+      load(xa, ya, q0 + (kWave * F::kStepVec));
       process_step<F>(st, p, pen, greedy, lse, nuc, spec, log2e_over_t, prow, xb, yb, q0, q_end);
-      if ((q0 += kStepQuads) >= q_end) break;
+      if ((q0 += (kWave * F::kStepVec)) >= q_end) break;
       pace(q0);
     }
     if (a.pace) __builtin_amdgcn_s_setprio(3);  // the rest is the row's critical path
