@@ -659,6 +659,10 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b
                     fg::kSpecMinK;
   }
   any_pen = any_pen && b->counts != nullptr;
+  // Speculation only runs over short slices (the kernel's own condition); a
+  // launch without it streams in shorter steps.
+  any_spec = any_spec && (a.wave_elems > a.wave_elems_b ? a.wave_elems : a.wave_elems_b) <=
+                             fg::kSpecMaxElems;
   const int bits = (any_pen ? 1 : 0) | (any_greedy ? 2 : 0) | (any_top ? 4 : 0) |
                    (b->logprobs ? 8 : 0) | (any_nuc ? 16 : 0) | (any_spec ? 32 : 0);
   const uint32_t grid = b->rows * chunks;
