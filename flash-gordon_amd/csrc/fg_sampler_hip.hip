@@ -127,12 +127,13 @@ hipError_t dense_launch(fg::DenseArgs a, uint32_t tokens, hipStream_t stream) {
 // Paired layout (a row's chunks split between the grid's halves) for grids
 // of at most this many workgroups (two per CU), and the share (per mille) of
 // a row its first-half chunks stream: measured on MI355X at V = 151,936,
-// 580 for two chunks per row (config 3: 79.5 -> 77.4 us), even for more
-// (config 2: 21.96 -> 21.67 us); grids of four workgroups per CU run slower
-// paired (config 4: 28.5 -> 30.8 us).
+// 580 for two chunks per row (config 3 at 2 chunks: 79.5 -> 77.4 us), 530
+// for more (config 2 at 8 chunks, 512-element steps: 21.1 us even, 20.65 at
+// 520, 20.5 at 530, 20.55 at 535); grids of four workgroups per CU run
+// slower paired (config 4: 28.5 -> 30.8 us).
 constexpr uint32_t kPairedMaxGroups = 512u;
 constexpr uint32_t kFrontPermilleTwo = 580u;
-constexpr uint32_t kFrontPermilleMany = 500u;
+constexpr uint32_t kFrontPermilleMany = 530u;
 
 namespace {
 
