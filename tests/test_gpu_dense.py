@@ -75,7 +75,7 @@ def test_reference_cooked_dense_case(dev):
 
 @pytest.mark.parametrize("width,rows,tokens", [(32, 1, 1), (64, 17, 3), (2560, 1000, 1),
                                                (2560, 4099, 2), (4096, 300, 5), (8192, 50, 1),
-                                               (96, 33, 4)])
+                                               (96, 33, 4), (2560, 500, 7)])
 def test_dense_matches_f64(dev, width, rows, tokens):
     rng = np.random.default_rng(width * 7 + rows)
     packed = packed_random(rng, width, rows)
@@ -101,7 +101,8 @@ def fused(dev, sl, cooked_slice, x, width, logits=True):
 
 
 @pytest.mark.parametrize("ways,way,width,vocab,tokens", [(4, 1, 320, 4096, 3), (2, 1, 2560, 4000, 2),
-                                                         (1, 0, 64, 1000, 1), (4, 3, 96, 999, 4)])
+                                                         (1, 0, 64, 1000, 1), (4, 3, 96, 999, 4),
+                                                         (2, 0, 2560, 3000, 7)])
 def test_fused_finalist_is_best_of_plain(dev, ways, way, width, vocab, tokens):
     rng = np.random.default_rng(ways * 100 + width)
     per = (vocab // ways) // 16 * 16
