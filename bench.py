@@ -357,7 +357,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the rows of a batch are independent "
-              "and would shard data-parallel over GPUs with no exchange (see DESIGN.md).",
+              "and would shard data-parallel over GPUs with no exchange.",
               file=sys.stderr)
         sys.exit(2)
 
