@@ -49,6 +49,8 @@ EXPORTS = (
     "fg_q8_0_cooked_tile_bytes", "fg_q8_0_cooked_matrix_bytes", "fg_cook_q8_0_rows",
     "fg_uncook_q8_0_rows", "fg_hip_dense_q8_0_cooked", "fg_hip_output_slice_run_dense",
     "fg_sampler_hip_plan", "fg_sampler_hip_block",
+    "fg_output_config_encode", "fg_output_config_decode", "fg_output_result_encode",
+    "fg_output_result_decode", "fg_output_configs_batch", "fg_output_results_encode_batch",
 )
 
 ROWS_NUCLEUS = 1
@@ -76,6 +78,19 @@ class SamplerConfig(C.Structure):
 
 class SamplerState(C.Structure):
     _fields_ = [("state", C.c_uint64)]
+
+
+class OutputConfig(C.Structure):
+    """fg_output_config (include/fg_output_wire.h)."""
+    _fields_ = [("source_rank", C.c_uint8), ("destination_rank", C.c_uint8),
+                ("flags", C.c_uint8), ("session_slot", C.c_uint8), ("token_index", C.c_uint32),
+                ("sampler", SamplerConfig), ("uniform", C.c_float)]
+
+
+class OutputResult(C.Structure):
+    """fg_output_result (include/fg_output_wire.h)."""
+    _fields_ = [("source_rank", C.c_uint8), ("destination_rank", C.c_uint8),
+                ("token_index", C.c_uint32), ("token", C.c_uint32), ("logit", C.c_float)]
 
 
 class Batch(C.Structure):
@@ -166,6 +181,12 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_hip_output_slice_run_dense":
             (C.c_int, [P, P, P, u32, u32, f32, P, P, P, P, P, E]),
         "fg_sampler_hip_plan": (C.c_int, [u32, u32, u32, C.POINTER(Geometry), E]),
+        "fg_output_config_encode": (C.c_int, [P, C.POINTER(OutputConfig), E]),
+        "fg_output_config_decode": (C.c_int, [C.POINTER(OutputConfig), P, u32, E]),
+        "fg_output_result_encode": (C.c_int, [P, C.POINTER(OutputResult), E]),
+        "fg_output_result_decode": (C.c_int, [C.POINTER(OutputResult), P, u32, E]),
+        "fg_output_configs_batch": (C.c_int, [P, u32, P, P, E]),
+        "fg_output_results_encode_batch": (C.c_int, [P, P, P, P, P, u32, C.POINTER(u32), E]),
         "fg_sampler_hip_block": (C.c_int, [C.POINTER(Geometry), u32, u32, u32, u32,
                                            C.POINTER(u32), C.POINTER(u32), C.POINTER(u32),
                                            C.POINTER(u32), E]),
