@@ -403,3 +403,42 @@ def test_paired_layout_shares(dev, monkeypatch, groups, share, k):
     else:
         check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), W.oracle_run(w),
               f"paired nucleus groups={groups} share={share}", NUC_BOUNDARY)
+
+
+@pytest.mark.parametrize("nucleus", [False, True])
+def test_graph_replays_match_eager(dev, nucleus):
+    """One sample call captured in a HIP graph (the launch allocates and
+    clears nothing: the row counters reset themselves) and replayed three
+    times, with eager launches on the same sampler and synchronizations in
+    between; every replay's tokens, logits and statuses equal the eager
+    call's, which match the oracle."""
+    import torch
+    rows = 16
+    w = W.config3(rows=rows) if nucleus else W.config2(rows=rows)
+    flags = fg_hip.ALLOW_FULL_VOCAB if nucleus else 0
+    s = fg_hip.HipSampler(W.V, rows)
+    eager = run_hip(w, dev, flags=flags, sampler=s)
+    check(w, eager, W.oracle_run(w), "eager", NUC_BOUNDARY if nucleus else BOUNDARY)
+    d_logits = to_dev(w["logits"], dev)
+    d_counts = to_dev(w["counts"], dev)
+    d_u = to_dev(w["uniforms"], dev)
+    tok = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+    tl = torch.zeros(rows, dtype=torch.float32, device=dev)
+    st = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            s.sample(d_logits, d_u, tok, counts=d_counts, token_logits=tl, row_status=st,
+                     stream=side.cuda_stream)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        tok.fill_(-1)
+        st.fill_(-1)
+        run_hip(w, dev, flags=flags, sampler=s)  # eager work on the same sampler between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(tok.cpu().numpy().view(np.uint32), eager["token"]), replay
+        assert np.array_equal(tl.cpu().numpy().view(np.uint32), eager["logit"].view(np.uint32)), replay
+        assert np.array_equal(st.cpu().numpy(), eager["status"]), replay
