@@ -332,7 +332,8 @@ __device__ __forceinline__ void lse_accumulate(double& m, double& z, double mi, 
 // exp(s - max) * (max - s)).  The terms are f32 exp2, each within
 // 1.2e-7 + 1.8e-7 |s - max| of exp (one ulp of v_exp_f32, plus the rounding of
 // s - max, of log2(e) and of the product), so e bounds their error.  A
-// streaming step sums its 16 terms per lane pairwise in f32 (four roundings,
+// streaming step (four quads per lane in launches with whole-row nucleus
+// rows) sums its 16 terms per lane pairwise in f32 (four roundings,
 // 2.4e-7 of the step's sum) before adding them in f64, so z is within
 // 3.6e-7 z + 1.8e-7 e of the exact sum.
 struct Mass {
