@@ -695,8 +695,10 @@ __device__ __forceinline__ void process_step(WaveState& st, const RowParams& p, 
       }
       st.nm = step_max;
     }
-    // The step's f32 terms summed pairwise in f32 (four roundings), then in
-    // f64; their error bound sum w * (max - s) in f32.
+    // The step's f32 terms summed pairwise in f32 (at most four roundings:
+    // the mass bound assumes no more), then in f64; their error bound
+    // sum w * (max - s) in f32.
+    static_assert(F::kStepVec <= 4, "the nucleus mass bound covers 16 terms per step");
     float w[F::kStepVec * 4];
     float ef = 0.0f;
 #pragma unroll
