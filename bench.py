@@ -252,6 +252,108 @@ def lm_head_bench(args, torch, fg_hip, dev):
         "wall_s": round(wall, 3)}))
 
 
+def timed(args, torch, stream, step):
+    """W untimed, then K timed calls of step() on `stream` (HIP events)."""
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / args.steps, time.perf_counter() - t0
+
+
+def history_bench(args, torch, fg_hip, dev):
+    """Count tables of config 2's batch rebuilt from FG_MSG_OUTPUT_HISTORY
+    payloads on the device (64 rows x 151,936, 1,024 Zipf(1.1) history ids
+    per row), the output-history path's per-session reset for a whole batch.
+    Algorithmic bytes: the cleared tables (4 B per count) plus the payloads."""
+    import numpy as np
+    rows, hist = ROWS, 1024
+    rng = np.random.default_rng(38)
+    ranks = np.arange(1, VOCAB + 1, dtype=np.float64)
+    p = ranks ** -1.1
+    p /= p.sum()
+    perm = rng.permutation(VOCAB)
+    payloads = [fg_hip.history_encode(perm[rng.choice(VOCAB, hist, p=p)], session_slot=0, vocab=VOCAB)
+                for _ in range(rows)]
+    offsets = np.zeros(rows + 1, dtype=np.int64)  # u64 byte offsets (the C signature)
+    offsets[1:] = np.cumsum([len(x) for x in payloads])
+    blob = torch.from_numpy(np.frombuffer(b"".join(payloads), dtype=np.uint8).copy()).to(dev)
+    d_off = torch.from_numpy(offsets).to(dev)
+    counts = torch.empty((rows, VOCAB), dtype=torch.int32, device=dev)
+    status = torch.empty(rows, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+    per_s, wall = timed(args, torch, stream, lambda: fg_hip.history_build_wire(
+        counts, VOCAB, VOCAB, blob, d_off, rows, status, stream=stream.cuda_stream))
+    assert int(status.abs().sum()) == 0
+    assert int(counts.sum()) == rows * hist
+    alg = 4 * rows * VOCAB + int(offsets[-1]) + 8 * (rows + 1)
+    print(json.dumps({
+        "metric": "history tables rebuilt/sec (64 rows x 151,936 from wire payloads)",
+        "value": round(1 / per_s, 1), "unit": "batches/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(per_s * 1e3, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32",
+        "data": "synthetic (1,024 Zipf(1.1) ids per row, seeded permutation of ranks)",
+        "config": {"workload": "history-build-wire-config2", "rows": rows, "vocab": VOCAB,
+                   "history": hist, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(alg / per_s / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(alg / per_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "fg::history_wire_clear_kernel",
+                     "algorithmic_bytes_per_launch": alg, "launch_us": round(per_s * 1e6, 3)},
+        "wall_s": round(wall, 3)}))
+
+
+def topk_reduce_bench(args, torch, fg_hip, dev):
+    """The QSA top-512 ladder (src/qsa.c:839-851) over 262,144 scores: one
+    fg_hip_topk_reduce per level until 512 remain (262,144 -> 32,768 ->
+    4,096 -> 512).  Algorithmic bytes per step: each level's scores and ids
+    read once and its 512-per-tile outputs written once."""
+    count = 262_144
+    g = torch.Generator(device=dev)
+    g.manual_seed(39)
+    scores = torch.randn(count, device=dev, generator=g)
+    bufs = [(torch.empty(count // 8, device=dev), torch.empty(count // 8, dtype=torch.int32, device=dev))
+            for _ in range(2)]
+    stream = torch.cuda.current_stream()
+    levels = []
+
+    def step():
+        s, ids, n, slot = scores, None, count, 0
+        while n > 512:
+            out_s, out_i = bufs[slot]
+            n = fg_hip.topk_reduce(out_s, out_i, s, ids, n, stream=stream.cuda_stream)
+            s, ids, slot = out_s, out_i, slot ^ 1
+        return s, ids
+
+    per_s, wall = timed(args, torch, stream, step)
+    s, ids = step()
+    torch.cuda.synchronize()
+    want = torch.topk(scores, 512).values
+    assert torch.equal(s[:512], want), "top-512 differs from torch.topk"
+    n, alg = count, 0
+    while n > 512:
+        tiles = (n + 4095) // 4096
+        alg += n * (4 if n == count else 8) + tiles * 512 * 8
+        n = tiles * 512
+    print(json.dumps({
+        "metric": "QSA top-512 ladders/sec (262,144 scores)",
+        "value": round(1 / per_s, 1), "unit": "ladders/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(per_s * 1e3, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (N(0,1) scores, ids implicit at the first level)",
+        "config": {"workload": "qsa-top512-ladder", "count": count, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(alg / per_s / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(alg / per_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "fg::topk_reduce_kernel",
+                     "algorithmic_bytes_per_launch": alg, "launch_us": round(per_s * 1e6, 3)},
+        "wall_s": round(wall, 3)}))
+
+
 def split_bench(args, torch, fg_hip, dev, w, sets, nsets, batch_bytes):
     ways, rows = args.split, w.rows
     quarter = VOCAB // ways
@@ -352,6 +454,10 @@ def main():
     ap.add_argument("--tokens", type=int, default=1, help="--lm-head: hidden vectors per step")
     ap.add_argument("--unfused", action="store_true",
                     help="--lm-head: the plain product writing logits (no finalist)")
+    ap.add_argument("--history", action="store_true",
+                    help="time the history count tables rebuilt from wire payloads")
+    ap.add_argument("--topk-reduce", action="store_true",
+                    help="time the QSA top-512 ladder over 262,144 scores")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 1 GiB device copy (the rocprof FETCH/WRITE_SIZE reference)")
     args = ap.parse_args()
@@ -380,6 +486,10 @@ def main():
 
     if args.lm_head:
         return lm_head_bench(args, torch, fg_hip, dev)
+    if args.history:
+        return history_bench(args, torch, fg_hip, dev)
+    if args.topk_reduce:
+        return topk_reduce_bench(args, torch, fg_hip, dev)
 
     w = Workload(args.config, fg_hip, sampled=not args.greedy)
     batch_bytes = 8 * VOCAB * w.rows

@@ -173,7 +173,13 @@ __global__ __launch_bounds__(256) void history_count_kernel(uint32_t* counts, ui
       atomicOr(bad, 1u);
       continue;
     }
-    saturating_increment(counts + static_cast<uint64_t>(r) * stride + id);
+    // A cleared row with fewer than UINT32_MAX ids cannot saturate: a plain
+    // atomic add avoids compare-and-swap retries on repeated ids.
+    uint32_t* c = counts + static_cast<uint64_t>(r) * stride + id;
+    if (e - b < 0xffffffffull)
+      atomicAdd(c, 1u);
+    else
+      saturating_increment(c);
   }
 }
 
@@ -193,12 +199,15 @@ __global__ __launch_bounds__(256) void history_increment_kernel(uint32_t* counts
 }
 
 // FG_MSG_OUTPUT_HISTORY payloads (src/protocol.c:1348-1366) decoded on the
-// device and turned into count tables (src/output.c:601-617), one row per
-// workgroup: validate the whole payload first, then clear the row and count.
-// A row that fails validation keeps its counts; its status says why
-// (FG_ERR_ARGUMENT: shorter than the header; FG_ERR_FORMAT: the decoder's
-// other checks).  Payload bytes are big-endian and need not be aligned.
-constexpr int kWireBlock = 1024;
+// device and turned into count tables (src/output.c:601-617), in two
+// launches: kWireChunks workgroups per row each validate the whole payload
+// and clear their part of the row (the first one writes the row's status),
+// then a counting launch adds the row's ids.  A row that fails validation
+// keeps its counts; its status says why (FG_ERR_ARGUMENT: shorter than the
+// header; FG_ERR_FORMAT: the decoder's other checks).  Payload bytes are
+// big-endian and need not be aligned.
+constexpr int kWireBlock = 256;
+constexpr uint32_t kWireChunks = 16u;  // clearing workgroups per row
 constexpr uint32_t kWireHeader = 8u;
 constexpr uint32_t kWireMaxCount = 262144u;
 constexpr uint32_t kWireMaxSlots = 2u;
@@ -208,17 +217,17 @@ __device__ __forceinline__ uint32_t load_be32(const uint8_t* p) {
          (static_cast<uint32_t>(p[2]) << 8) | static_cast<uint32_t>(p[3]);
 }
 
-__global__ __launch_bounds__(kWireBlock) void history_wire_kernel(
-    uint32_t* counts, uint64_t stride, uint32_t vocab, const uint8_t* payloads,
-    const uint64_t* offsets, int32_t* row_status, uint8_t* row_slot) {
+// Status of row r's payload (0, 2 or 4) and its id count; every thread of
+// the workgroup returns the same.
+__device__ inline int32_t wire_validate(const uint8_t* p, uint64_t bytes, uint32_t vocab,
+                                        uint32_t* count_out, uint8_t* slot_out) {
   __shared__ int32_t s_status;
   __shared__ uint32_t s_count;
-  const uint32_t r = blockIdx.x;
-  const uint8_t* p = payloads + offsets[r];
-  const uint64_t bytes = offsets[r + 1] - offsets[r];
+  __shared__ uint8_t s_slot;
   if (threadIdx.x == 0) {
     int32_t st = 0;
     uint32_t count = 0u;
+    uint8_t slot = 0u;
     if (bytes < kWireHeader) {
       st = 2;  // FG_ERR_ARGUMENT
     } else {
@@ -228,24 +237,62 @@ __global__ __launch_bounds__(kWireBlock) void history_wire_kernel(
       if (reserved || p[4] >= kWireMaxSlots || count > kWireMaxCount ||
           kWireHeader + 4ull * count != bytes)
         st = 4;  // FG_ERR_FORMAT
-      if (row_slot) row_slot[r] = st == 0 ? p[4] : 0u;
+      slot = p[4];
     }
     s_status = st;
     s_count = st == 0 ? count : 0u;
+    s_slot = st == 0 ? slot : 0u;
   }
   __syncthreads();
   const uint32_t count = s_count;
   for (uint32_t i = threadIdx.x; i < count; i += kWireBlock)
     if (load_be32(p + kWireHeader + 4u * i) >= vocab) atomicOr(&s_status, 4);
   __syncthreads();
-  const int32_t st = s_status;
-  if (threadIdx.x == 0) row_status[r] = st;
+  *count_out = count;
+  *slot_out = s_slot;
+  return s_status;
+}
+
+// Grid kWireChunks * rows: workgroup b clears chunk b % kWireChunks of row
+// b / kWireChunks.
+__global__ __launch_bounds__(kWireBlock) void history_wire_clear_kernel(
+    uint32_t* counts, uint64_t stride, uint32_t vocab, const uint8_t* payloads,
+    const uint64_t* offsets, int32_t* row_status, uint8_t* row_slot) {
+  const uint32_t r = blockIdx.x / kWireChunks;
+  const uint32_t chunk = blockIdx.x - r * kWireChunks;
+  const uint8_t* p = payloads + offsets[r];
+  uint32_t count;
+  uint8_t slot;
+  const int32_t st = wire_validate(p, offsets[r + 1] - offsets[r], vocab, &count, &slot);
+  if (chunk == 0 && threadIdx.x == 0) {
+    row_status[r] = st;
+    if (row_slot && st != 2) row_slot[r] = slot;
+  }
   if (st != 0) return;
+  const uint32_t per = (vocab + kWireChunks - 1u) / kWireChunks;
+  const uint32_t begin = chunk * per;
+  const uint32_t end = begin + per < vocab ? begin + per : vocab;
   uint32_t* crow = counts + static_cast<uint64_t>(r) * stride;
-  for (uint32_t i = threadIdx.x; i < vocab; i += kWireBlock) crow[i] = 0u;
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < count; i += kWireBlock)
-    saturating_increment(crow + load_be32(p + kWireHeader + 4u * i));
+  for (uint32_t i = begin + threadIdx.x; i < end; i += kWireBlock) crow[i] = 0u;
+}
+
+// Grid kWireCountGroups * rows: the ids of each valid row, once the clearing
+// launch is done.
+constexpr uint32_t kWireCountGroups = 8u;
+__global__ __launch_bounds__(kWireBlock) void history_wire_count_kernel(
+    uint32_t* counts, uint64_t stride, const uint8_t* payloads, const uint64_t* offsets,
+    const int32_t* row_status) {
+  const uint32_t r = blockIdx.x / kWireCountGroups;
+  const uint32_t g = blockIdx.x - r * kWireCountGroups;
+  if (row_status[r] != 0) return;
+  const uint8_t* p = payloads + offsets[r];
+  const uint32_t count = load_be32(p);
+  uint32_t* crow = counts + static_cast<uint64_t>(r) * stride;
+  // The row was cleared and holds at most kWireMaxCount ids, so no count can
+  // reach UINT32_MAX: a plain atomic add saturates nothing and keeps hot ids
+  // (a Zipf history repeats its head tokens) free of compare-and-swap retries.
+  for (uint32_t i = g * kWireBlock + threadIdx.x; i < count; i += kWireCountGroups * kWireBlock)
+    atomicAdd(crow + load_be32(p + kWireHeader + 4u * i), 1u);
 }
 
 // Top-512 reduction of shaders/fg_topk_reduce_v2.comp (src/vk.c:2235): per

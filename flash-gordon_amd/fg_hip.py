@@ -266,7 +266,15 @@ def topk_reduce(out_scores, out_ids, in_scores, in_ids, count, stream=None) -> i
     return n.value
 
 
+def _check_u64_offsets(offsets, rows):
+    """The history entry points take `const uint64_t *offsets` (rows + 1)."""
+    size = getattr(offsets, "element_size", None)
+    if size is not None and (size() != 8 or offsets.numel() < rows + 1):
+        raise ValueError("offsets must hold rows + 1 64-bit entries")
+
+
 def history_build(counts, stride, vocab, ids, offsets, rows, stream=None):
+    _check_u64_offsets(offsets, rows)
     err = FgError()
     _check(lib().fg_hip_history_build(_ptr(counts), stride, vocab, _ptr(ids), _ptr(offsets),
                                       rows, _stream(stream), C.byref(err)), err)
@@ -275,6 +283,7 @@ def history_build(counts, stride, vocab, ids, offsets, rows, stream=None):
 def history_build_wire(counts, stride, vocab, payloads, offsets, rows, row_status,
                        row_slot=None, stream=None):
     """fg_hip_history_build_wire: count tables from FG_MSG_OUTPUT_HISTORY payloads."""
+    _check_u64_offsets(offsets, rows)
     err = FgError()
     _check(lib().fg_hip_history_build_wire(_ptr(counts), stride, vocab, _ptr(payloads),
                                            _ptr(offsets), rows, _ptr(row_status),

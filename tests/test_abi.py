@@ -53,3 +53,17 @@ def test_missing_library_fails_loudly(tmp_path):
     import pytest
     with pytest.raises(RuntimeError, match="not built"):
         fg_hip.load_library(tmp_path / "nope.so")
+
+
+def test_history_offsets_must_be_64_bit():
+    """The history entry points read `const uint64_t *offsets`: the binding
+    refuses narrower offsets before any device call."""
+    import pytest
+    import torch
+    off32 = torch.zeros(5, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        fg_hip.history_build_wire(None, 8, 8, None, off32, 4, None)
+    with pytest.raises(ValueError):
+        fg_hip.history_build(None, 8, 8, None, off32, 4)
+    with pytest.raises(ValueError):
+        fg_hip.history_build(None, 8, 8, None, torch.zeros(4, dtype=torch.int64), 4)
