@@ -307,27 +307,103 @@ constexpr int kReduceBlock = 512;
 constexpr uint32_t kReduceTile = 4096u;
 constexpr uint32_t kReduceKeep = 512u;
 
+// Per tile: a radix select (eight 8-bit digits, most significant first)
+// finds the composite of the tile's min(512, n)-th entry, the entries at or
+// above it are compacted into LDS, and only those are sorted.
 __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
     float* out_scores, uint32_t* out_ids, const float* in_scores, const uint32_t* in_ids,
     uint32_t count, uint32_t out_per_tile) {
-  __shared__ uint64_t s_key[kReduceTile];
-  __shared__ uint16_t s_pos[kReduceTile];
+  constexpr uint32_t kPer = kReduceTile / kReduceBlock;  // entries per thread
+  __shared__ uint32_t s_hist[256];
+  __shared__ uint32_t s_sel[2];  // chosen digit, entries above it
+  __shared__ uint64_t s_key[kReduceKeep];
+  __shared__ uint16_t s_pos[kReduceKeep];
+  __shared__ uint32_t s_n;
   const uint32_t tid = threadIdx.x;
   const uint32_t base = blockIdx.x * kReduceTile;
   const uint32_t n = min(kReduceTile, count - base);
-  uint32_t P = 1u;
-  while (P < n) P <<= 1;
-  for (uint32_t i = tid; i < P; i += kReduceBlock) {
-    uint64_t k = 0ull;
+  uint64_t key[kPer];
+#pragma unroll
+  for (uint32_t e = 0; e < kPer; e++) {
+    const uint32_t i = e * kReduceBlock + tid;
+    uint64_t k = 0ull;  // a fill slot of a partial tile: never selected
     if (i < n) {
       const uint32_t id = in_ids ? in_ids[base + i] : base + i;
-      // Padding ids rank last among the entries (1) but above the fill
-      // slots of a partial tile (0), which must never reach the output.
+      // Padding ids rank last among the entries (1).
       k = id == kInvalidId ? 1ull : greedy_comp(in_scores[base + i], id);
     }
-    s_key[i] = k;
-    s_pos[i] = static_cast<uint16_t>(i);
+    key[e] = k;
   }
+  const uint32_t want = min(kReduceKeep, n);
+  // Radix select: after digit d, `prefix` holds the top d bytes of the
+  // want-th largest key and `rank` its rank among the keys sharing them.
+  uint64_t prefix = 0ull;
+  uint32_t rank = want;
+  for (int d = 7; d >= 0; d--) {
+    const uint32_t shift = 8u * static_cast<uint32_t>(d);
+    const uint64_t hi_mask = d == 7 ? 0ull : ~0ull << (shift + 8u);
+    if (tid < 256u) s_hist[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; e++) {
+      const uint32_t i = e * kReduceBlock + tid;
+      if (i < n && (key[e] & hi_mask) == prefix)
+        atomicAdd(&s_hist[(key[e] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 64u) {
+      // Bins from the top: lane l owns bins 255 - 4l .. 252 - 4l.
+      uint32_t c[4];
+      uint32_t sum = 0u;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        c[b] = s_hist[255u - 4u * tid - b];
+        sum += c[b];
+      }
+      uint32_t before = sum;  // inclusive prefix over lanes, then made exclusive
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(before, o, 64);
+        if (tid >= static_cast<uint32_t>(o)) before += t;
+      }
+      before -= sum;
+      uint32_t acc = before;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        if (acc < rank && acc + c[b] >= rank) {
+          s_sel[0] = 255u - 4u * tid - b;
+          s_sel[1] = acc;
+        }
+        acc += c[b];
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<uint64_t>(s_sel[0]) << shift;
+    rank -= s_sel[1];
+    __syncthreads();
+  }
+  // prefix is the want-th largest key; `rank` entries equal to it are kept.
+  if (tid == 0) {
+    s_n = 0u;
+    s_sel[0] = 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t e = 0; e < kPer; e++) {
+    const uint32_t i = e * kReduceBlock + tid;
+    bool keep = i < n && key[e] > prefix;
+    if (i < n && key[e] == prefix) keep = atomicAdd(&s_sel[0], 1u) < rank;
+    if (keep) {
+      const uint32_t at = atomicAdd(&s_n, 1u);
+      s_key[at] = key[e];
+      s_pos[at] = static_cast<uint16_t>(i);
+    }
+  }
+  __syncthreads();
+  // Sort the kept entries (want of them), padded to a power of two with 0.
+  uint32_t P = 1u;
+  while (P < want) P <<= 1;
+  for (uint32_t i = want + tid; i < P; i += kReduceBlock) s_key[i] = 0ull;
   __syncthreads();
   for (uint32_t k = 2u; k <= P; k <<= 1) {
     for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
@@ -347,10 +423,9 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
       __syncthreads();
     }
   }
-  const uint32_t valid = min(kReduceKeep, n);
   for (uint32_t i = tid; i < out_per_tile; i += kReduceBlock) {
     const uint64_t o = static_cast<uint64_t>(blockIdx.x) * kReduceKeep + i;
-    if (i < valid) {
+    if (i < want) {
       const uint32_t src = base + s_pos[i];
       out_scores[o] = in_scores[src];
       out_ids[o] = in_ids ? in_ids[src] : src;
