@@ -315,7 +315,7 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
     uint32_t count, uint32_t out_per_tile) {
   constexpr uint32_t kPer = kReduceTile / kReduceBlock;  // entries per thread
   __shared__ uint32_t s_hist[256];
-  __shared__ uint32_t s_sel[2];  // chosen digit, entries above it
+  __shared__ uint32_t s_sel[3];  // chosen digit, entries above it, entries in it
   __shared__ uint64_t s_key[kReduceKeep];
   __shared__ uint16_t s_pos[kReduceKeep];
   __shared__ uint32_t s_n;
@@ -339,6 +339,7 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
   // want-th largest key and `rank` its rank among the keys sharing them.
   uint64_t prefix = 0ull;
   uint32_t rank = want;
+  int last = 0;  // lowest digit selected: 4 when the top 32 bits settle it
   for (int d = 7; d >= 0; d--) {
     const uint32_t shift = 8u * static_cast<uint32_t>(d);
     const uint64_t hi_mask = d == 7 ? 0ull : ~0ull << (shift + 8u);
@@ -373,6 +374,7 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
         if (acc < rank && acc + c[b] >= rank) {
           s_sel[0] = 255u - 4u * tid - b;
           s_sel[1] = acc;
+          s_sel[2] = c[b];
         }
         acc += c[b];
       }
@@ -380,9 +382,16 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
     __syncthreads();
     prefix |= static_cast<uint64_t>(s_sel[0]) << shift;
     rank -= s_sel[1];
+    const bool settled = d == 4 && s_sel[2] == rank;  // keep every key of this float key
     __syncthreads();
+    if (settled) {
+      last = 4;
+      break;
+    }
   }
-  // prefix is the want-th largest key; `rank` entries equal to it are kept.
+  // Kept: keys above prefix, and `rank` keys equal to it in the digits
+  // selected (all of them when the float key settled it).
+  const uint64_t cmp_mask = last == 4 ? ~0ull << 32 : ~0ull;
   if (tid == 0) {
     s_n = 0u;
     s_sel[0] = 0u;
@@ -391,8 +400,9 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
 #pragma unroll
   for (uint32_t e = 0; e < kPer; e++) {
     const uint32_t i = e * kReduceBlock + tid;
-    bool keep = i < n && key[e] > prefix;
-    if (i < n && key[e] == prefix) keep = atomicAdd(&s_sel[0], 1u) < rank;
+    const uint64_t km = key[e] & cmp_mask;
+    bool keep = i < n && km > prefix;
+    if (i < n && km == prefix) keep = atomicAdd(&s_sel[0], 1u) < rank;
     if (keep) {
       const uint32_t at = atomicAdd(&s_n, 1u);
       s_key[at] = key[e];
