@@ -164,11 +164,11 @@ Tuning tuning_from_env() {
 // Chunking (measured on MI355X, V = 151,936): ceil(512 / rows) chunks, two
 // workgroups per CU (config 2's 64 rows: 8 chunks, 21.5 us against 25.2 at
 // 12; config 4's 128 rows: 4 chunks, 28.0 us against 29.2 at 6 and 29.9-31.1
-// at 8; one row: 64, 5.97 us against 6.35 at 128).  Launches with
-// whole-row nucleus rows (an exp per
-// element) take ceil(768 / rows), three per CU (config 3's 256 rows: 3
-// chunks 69.1 us against 72.7 at 2 and 85.6 at 4).  At most kMaxChunks per
-// row; each wave slice a multiple of 4 elements.
+// at 8; one row: 64 chunks, 5.97 us against 6.35 at 128).  Launches with
+// whole-row nucleus rows (an exp per element) take ceil(768 / rows), three
+// per CU (config 3's 256 rows: 3 chunks 69.1 us against 72.7 at 2 and 85.6
+// at 4).  At most kMaxChunks per row; each wave slice a multiple of 4
+// elements.
 //
 // Layout: the first workgroup dispatched to a CU streams faster than the
 // second (measured: ~8% at 8 chunks of V = 151,936 per row, ~12% at 2).
