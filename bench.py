@@ -28,8 +28,9 @@ runs the default.
 
 Output: one JSON line (see the repository's bench contract), with `roofline`
 (dominant kernel: algorithmic bytes / HIP-event launch time vs the 8 TB/s HBM
-peak) and, for config 2, `cpu_baseline` (the C oracle on the host cores over
-a bounded sample of the same batch).
+peak), `parity` (batch 0 checked against the C oracle; the run fails on a
+mismatch) and `cpu_baseline` (the C oracle on every host core over a bounded
+sample of the same batch, with the single-core figure beside it).
 """
 from __future__ import annotations
 
@@ -51,8 +52,14 @@ METRIC = "sampled rows/sec @ vocab 151,936, batch 64; achieved HBM GB/s vs peak"
 TRAFFIC_FILE = ROOT / "profiles" / "sample_rows_config2_traffic.json"
 
 
-def cfg(fg_hip, t, p, k, pres=0.0, freq=0.0, rep=1.0):
-    return fg_hip.make_config(t, p, k, presence=pres, frequency=freq, repetition=rep)
+class cfg(dict):
+    """One row's controls as the oracle's dict; `.c` is the C struct the
+    sampler takes."""
+
+    def __init__(self, fg_hip, t, p, k, pres=0.0, freq=0.0, rep=1.0):
+        super().__init__(temperature=t, top_p=p, top_k=k, presence=pres, frequency=freq,
+                         repetition=rep)
+        self.c = fg_hip.make_config(t, p, k, presence=pres, frequency=freq, repetition=rep)
 
 
 def zipf_counts(torch, g, dev, rows, draws, perm):
@@ -150,39 +157,64 @@ class Workload:
         return x.float().contiguous(), c.contiguous(), u
 
 
-def cpu_baseline(x, c, u, gpu_tokens, budget_s):
-    """The C oracle (oracle/, a restatement of the reference semantics) on this
-    host's cores over a bounded sample of batch 0; also cross-checks the GPU's
-    tokens for that batch."""
+def host_cores():
+    return len(os.sched_getaffinity(0))
+
+
+def oracle_parity(w, x, c, u, gpu_tokens, gpu_status, lp=None):
+    """Batch 0 of the run checked against the C oracle (oracle/, a restatement
+    of the reference semantics): token ids bit-exact unless the oracle's draw
+    lies within 1e-6 of a cumulative-probability boundary, row status equal,
+    log-probs within 1e-5.  Raises on any mismatch."""
+    import numpy as np
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle_ffi as O
 
-    cfgs = [dict(temperature=0.7, top_p=0.8, top_k=20, presence=1.5, frequency=0.0,
-                 repetition=1.05)] * ROWS
-    ref = O.sample_rows(cfgs, x, u, counts=c, threads=1)
+    ref = O.sample_rows(list(w.configs), x, u, counts=c, logprobs=w.logprobs,
+                        threads=host_cores())
+    assert (ref["status"] == gpu_status).all(), "row status differs from the oracle"
     same = (ref["token"] == gpu_tokens) | (ref["margin"] < 1e-6)
-    parity = f"{int(same.sum())}/{ROWS} rows match the oracle (bit-exact ids, 1e-6 boundary clause)"
+    assert same.all(), f"{int((~same).sum())}/{w.rows} rows differ from the oracle"
+    if lp is not None:
+        vals, ids = lp
+        err = float(np.abs(vals - ref["lp_values"]).max())
+        assert err <= 1e-5, f"log-probs differ from the oracle by {err}"
+        # Ids may swap only between equal values.
+        swapped = ids != ref["lp_ids"]
+        assert (np.abs(vals - ref["lp_values"])[swapped] <= 1e-5).all()
+    return (f"{w.rows}/{w.rows} rows of batch 0 match the oracle "
+            f"(bit-exact ids, 1e-6 boundary clause: {int((ref['token'] != gpu_tokens).sum())} used)")
+
+
+def cpu_baseline(w, x, c, u, budget_s):
+    """The C oracle timed on this host's cores over a bounded sample of
+    batch 0: half the budget on every core the process may run on, half on
+    one core."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle_ffi as O
+
+    cfgs = list(w.configs)
 
     def timed(threads, budget):
         rows = 0
         t0 = time.perf_counter()
         while True:
-            O.sample_rows(cfgs, x, u, counts=c, threads=threads)
-            rows += ROWS
+            O.sample_rows(cfgs, x, u, counts=c, logprobs=w.logprobs, threads=threads)
+            rows += w.rows
             el = time.perf_counter() - t0
             if el >= budget:
                 return rows / el, rows, el
 
     single, rows1, el1 = timed(1, budget_s / 2)
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads = host_cores()
     multi, rows_n, el_n = timed(threads, budget_s / 2)
     return {
         "value": round(multi, 1), "unit": "rows/s", "cores": threads, "kind": "port",
-        "sample": (f"batch 0 of the bench workload (64 rows x 151,936), repeated: {rows_n} rows "
-                   f"in {el_n:.1f} s on {threads} threads; single core {single:.1f} rows/s "
-                   f"({rows1} rows in {el1:.1f} s)"),
+        "sample": (f"batch 0 of the bench workload ({w.rows} rows x 151,936), repeated: "
+                   f"{rows_n} rows in {el_n:.1f} s on all {threads} host cores; single core "
+                   f"{single:.1f} rows/s ({rows1} rows in {el1:.1f} s)"),
         "single_core_value": round(single, 1),
-    }, parity
+    }
 
 
 LM_VOCAB, LM_WIDTH = 248_320, 2_560
@@ -504,18 +536,20 @@ def main():
 
     sampler = fg_hip.HipSampler(VOCAB, w.rows)
     stream = torch.cuda.current_stream()
-    sampler.set_configs(w.configs, flags=w.flags, stream=stream.cuda_stream)
-    tokens = torch.empty((nsets, w.rows), dtype=torch.int32, device=dev)
-    status = torch.empty((nsets, w.rows), dtype=torch.int32, device=dev)
+    sampler.set_configs([c.c for c in w.configs], flags=w.flags, stream=stream.cuda_stream)
+    # Sentinels: a set the run never reaches keeps them, and only the sets
+    # the run wrote are checked.
+    tokens = torch.full((nsets, w.rows), -1, dtype=torch.int32, device=dev)
+    status = torch.full((nsets, w.rows), -12345, dtype=torch.int32, device=dev)
     L = w.logprobs
-    lpv = torch.empty((w.rows, max(L, 1)), dtype=torch.float32, device=dev)
-    lpi = torch.empty((w.rows, max(L, 1)), dtype=torch.int32, device=dev)
+    lpv = torch.empty((nsets if L else 1, w.rows, max(L, 1)), dtype=torch.float32, device=dev)
+    lpi = torch.empty((nsets if L else 1, w.rows, max(L, 1)), dtype=torch.int32, device=dev)
 
     def step(i):
         k = i % nsets
         x, c, u = sets[k]
         sampler.sample(x, u, tokens[k], counts=c, row_status=status[k], logprobs=L,
-                       logprob_values=lpv if L else None, logprob_ids=lpi if L else None,
+                       logprob_values=lpv[k] if L else None, logprob_ids=lpi[k] if L else None,
                        stream=stream.cuda_stream)
 
     for i in range(args.warmup):
@@ -526,7 +560,7 @@ def main():
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(args.steps):
-        step(i)
+        step(args.warmup + i)
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -534,8 +568,14 @@ def main():
     per_launch_s = ms / 1e3 / args.steps
     rows_per_s = w.rows * args.steps / (ms / 1e3)
     achieved = w.alg_bytes / per_launch_s / 1e9
-    bad = int((status != 0).sum())
-    assert bad == 0, f"{bad} rows reported errors"
+    written = min(nsets, args.warmup + args.steps)
+    bad = int((status[:written] != 0).sum())
+    assert bad == 0, f"{bad} rows of {written} written sets reported errors"
+    x0, c0, u0 = (t.cpu().numpy() for t in sets[0])
+    c0 = c0.view("uint32")
+    parity = oracle_parity(
+        w, x0, c0, u0, tokens[0].cpu().numpy().view("uint32"), status[0].cpu().numpy(),
+        (lpv[0].cpu().numpy(), lpi[0].cpu().numpy().view("uint32")) if L else None)
 
     traffic = None
     if args.config == 2 and TRAFFIC_FILE.exists():
@@ -566,13 +606,9 @@ def main():
                      "launch_us": round(per_launch_s * 1e6, 3)},
         "wall_s": round(wall, 3),
     }
-    if args.config == 2 and not args.no_cpu:
-        x, c, u = sets[0]
-        g_tok = tokens[0].cpu().numpy().view("uint32")
-        cpu, parity = cpu_baseline(x.cpu().numpy(), c.cpu().numpy().view("uint32"),
-                                   u.cpu().numpy(), g_tok, args.cpu_seconds)
-        line["cpu_baseline"] = cpu
-        line["parity"] = parity
+    line["parity"] = parity
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(w, x0, c0, u0, args.cpu_seconds)
     print(json.dumps(line))
 
 

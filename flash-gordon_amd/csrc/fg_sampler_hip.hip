@@ -217,12 +217,21 @@ void plan_geometry(uint32_t vocab, uint32_t rows, bool nuc_rows, bool same_cost,
 
 }  // namespace
 
+// set_configs stages each upload in its own pinned slot and records an event
+// after the copy; a slot is rewritten only after its event, so a caller that
+// changes every row's controls on every step never waits for the stream
+// unless kStageSlots uploads are still in flight.
+constexpr uint32_t kStageSlots = 8;
+
 struct fg_sampler_hip {
   int device;
   uint32_t vocab;
   uint32_t max_rows;
   RowParams* d_params;      // [max_rows]
-  RowParams* h_params;      // host mirror of the uploaded table
+  RowParams* h_params;      // host mirror of the uploaded table (launch-variant choice)
+  RowParams* h_stage;       // pinned [kStageSlots][max_rows]: copy sources of set_configs
+  hipEvent_t stage_done[kStageSlots];  // recorded after each slot's copy
+  uint32_t stage_next;      // slot the next set_configs fills
   uint32_t config_rows;     // rows configured by the last set_configs
   uint64_t slots;           // wave slots in the workspace
   uint64_t* d_cand;         // [slots][kMaxK]
@@ -532,6 +541,11 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMalloc(&s->d_nuc_deep, sizeof(uint32_t) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&s->d_nuc_max, sizeof(float) * max_rows);
   if (e == hipSuccess) e = hipMemset(s->d_params, 0, sizeof(RowParams) * max_rows);
+  if (e == hipSuccess)
+    e = hipHostMalloc(reinterpret_cast<void**>(&s->h_stage),
+                      sizeof(RowParams) * max_rows * kStageSlots, hipHostMallocDefault);
+  for (uint32_t i = 0; i < kStageSlots && e == hipSuccess; i++)
+    e = hipEventCreateWithFlags(&s->stage_done[i], hipEventDisableTiming);
 #ifdef FG_SAMPLE_TRACE
   if (e == hipSuccess) e = hipMalloc(&s->trace, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
   if (e == hipSuccess) e = hipMemset(s->trace, 0, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
@@ -561,6 +575,14 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   (void)hipFree(s->d_nuc_deep);
   (void)hipFree(s->d_nuc_max);
   (void)hipFree(s->trace);
+  // Pending uploads read the pinned slots: let them finish first.
+  for (uint32_t i = 0; i < kStageSlots; i++) {
+    if (s->stage_done[i]) {
+      (void)hipEventSynchronize(s->stage_done[i]);
+      (void)hipEventDestroy(s->stage_done[i]);
+    }
+  }
+  (void)hipHostFree(s->h_stage);
   free(s->h_params);
   free(s);
 }
@@ -588,10 +610,19 @@ fg_status fg_sampler_hip_set_configs(fg_sampler_hip* s, const fg_sampler_config*
     p.flags = fg_sampler_penalties_active(c) ? fg::kRowPenalties : 0u;
     s->h_params[r] = p;
   }
-  hipError_t e = hipMemcpyAsync(s->d_params, s->h_params, sizeof(RowParams) * rows,
-                                hipMemcpyHostToDevice, as_stream(stream));
-  if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+  // The copy is ordered on `stream` after earlier launches that read
+  // d_params and before later ones; only its pinned source needs guarding.
+  const uint32_t slot = s->stage_next;
+  RowParams* src = s->h_stage + static_cast<size_t>(slot) * s->max_rows;
+  hipError_t e = hipEventSynchronize(s->stage_done[slot]);
+  if (e == hipSuccess) {
+    memcpy(src, s->h_params, sizeof(RowParams) * rows);
+    e = hipMemcpyAsync(s->d_params, src, sizeof(RowParams) * rows, hipMemcpyHostToDevice,
+                       as_stream(stream));
+  }
+  if (e == hipSuccess) e = hipEventRecord(s->stage_done[slot], as_stream(stream));
   if (e != hipSuccess) return hip_fail(err, e, "upload sampler configuration");
+  s->stage_next = (slot + 1u) % kStageSlots;
   s->config_rows = rows;
   return FG_OK;
 }

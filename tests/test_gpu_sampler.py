@@ -115,9 +115,86 @@ def test_config4_ties(dev, sampled):
     check(w, run_hip(w, dev), W.oracle_run(w), f"config4 sampled={sampled}")
 
 
+def cores():
+    import os
+    return len(os.sched_getaffinity(0))
+
+
 def test_config5_logprobs(dev):
     w = W.config5(rows=64)
-    check(w, run_hip(w, dev), W.oracle_run(w), "config5")
+    check(w, run_hip(w, dev), W.oracle_run(w, threads=cores()), "config5")
+
+
+def test_config5_full_batch(dev):
+    """Config 5 at its stated batch: 1,024 rows, which the launch rule runs at
+    one workgroup per row (the row merged in LDS, no cross-workgroup
+    hand-off), with top-k 64 and 20 log-probs."""
+    assert fg_hip.plan(W.V, 1024).chunks == 1
+    w = W.config5()
+    check(w, run_hip(w, dev), W.oracle_run(w, threads=cores()), "config5 1024 rows")
+
+
+@pytest.mark.parametrize("k,logprobs", [(20, 0), (64, 20), (0, 0)])
+def test_one_chunk_rows_full_vocab(dev, monkeypatch, k, logprobs):
+    """One workgroup per row at V=151,936 forced on a 64-row batch
+    (FG_HIP_TARGET_GROUPS=64): top-k 20, top-k 64 with log-probs and the
+    whole-row nucleus, all through the single-chunk finish."""
+    monkeypatch.setenv("FG_HIP_TARGET_GROUPS", "64")
+    assert fg_hip.plan(W.V, 64).chunks == 1
+    w = W.config5(rows=64)
+    w["logprobs"] = logprobs
+    flags = 0
+    if k == 0:
+        w = W.config3(rows=64)
+        flags = fg_hip.ALLOW_FULL_VOCAB
+    else:
+        w["configs"] = [dict(c, top_k=k) for c in w["configs"]]
+    check(w, run_hip(w, dev, flags=flags), W.oracle_run(w, threads=cores()),
+          f"one chunk k={k}", NUC_BOUNDARY if k == 0 else BOUNDARY)
+
+
+def test_owner_loop_controls_change_every_call(dev):
+    """The output owner's loop: every row's controls (temperature, top-p,
+    top-k, penalties, greedy rows) and uniforms change on every call, with
+    set_configs before each sample and no synchronisation anywhere in the
+    loop; each call's results match the oracle run with that call's
+    controls."""
+    import torch
+    rows, calls = 16, 10
+    base = W.config2(rows=rows)
+    rng = np.random.default_rng(7)
+    s = fg_hip.HipSampler(W.V, rows)
+    d_logits = to_dev(base["logits"], dev)
+    d_counts = to_dev(base["counts"], dev)
+    plans = []
+    toks = torch.full((calls, rows), -1, dtype=torch.int32, device=dev)
+    tls = torch.zeros((calls, rows), dtype=torch.float32, device=dev)
+    sts = torch.full((calls, rows), -1, dtype=torch.int32, device=dev)
+    d_us = []
+    torch.cuda.synchronize()
+    for i in range(calls):
+        cfgs = []
+        for r in range(rows):
+            if rng.random() < 0.2:
+                cfgs.append(W.cfg(0.0, 1.0, 1, repetition=float(rng.choice([1.0, 1.1]))))
+            else:
+                cfgs.append(W.cfg(float(rng.uniform(0.2, 1.5)), float(rng.uniform(0.3, 1.0)),
+                                  int(rng.integers(1, 65)), presence=float(rng.uniform(0, 2)),
+                                  frequency=float(rng.uniform(0, 1)),
+                                  repetition=float(rng.uniform(0.9, 1.2))))
+        u = rng.random(rows).astype(np.float32)
+        d_u = torch.from_numpy(u).to(dev, non_blocking=False)
+        d_us.append(d_u)
+        s.set_configs([fg_hip.make_config(c["temperature"], c["top_p"], c["top_k"], c["presence"],
+                                          c["frequency"], c["repetition"]) for c in cfgs])
+        s.sample(d_logits, d_u, toks[i], counts=d_counts, token_logits=tls[i], row_status=sts[i])
+        plans.append((cfgs, u))
+    torch.cuda.synchronize()
+    for i, (cfgs, u) in enumerate(plans):
+        w = dict(base, configs=cfgs, uniforms=u)
+        got = dict(token=toks[i].cpu().numpy().view(np.uint32), logit=tls[i].cpu().numpy(),
+                   status=sts[i].cpu().numpy())
+        check(w, got, W.oracle_run(w, threads=cores()), f"owner call {i}")
 
 
 def test_mixed_rows_and_greedy_logprobs(dev):
@@ -242,9 +319,19 @@ def test_history_increment(dev):
 
 def test_config3_whole_row_nucleus(dev):
     w = W.config3(rows=64)
-    ref = W.oracle_run(w)
+    ref = W.oracle_run(w, threads=cores())
     assert (ref["cutoff"] <= 64).all()
     check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), ref, "config3", NUC_BOUNDARY)
+
+
+def test_config3_full_batch(dev):
+    """Config 3 at its stated batch: 256 rows, three unpaired chunks per row
+    (the nucleus launch rule)."""
+    g = fg_hip.plan(W.V, 256, fg_hip.ROWS_NUCLEUS)
+    assert (g.chunks, g.split) == (3, 3)
+    w = W.config3()
+    check(w, run_hip(w, dev, flags=fg_hip.ALLOW_FULL_VOCAB), W.oracle_run(w, threads=cores()),
+          "config3 256 rows", NUC_BOUNDARY)
 
 
 def test_nucleus_cut_depths(dev):
