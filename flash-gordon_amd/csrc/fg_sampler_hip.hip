@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+
+#include <atomic>
 #include <stdlib.h>
 #include <string.h>
 
@@ -217,6 +219,24 @@ void plan_geometry(uint32_t vocab, uint32_t rows, bool nuc_rows, bool same_cost,
 
 }  // namespace
 
+// Device workspace of one sampling launch: the per-row controls and the
+// hand-off buffers of the fused kernel (see fg::SampleArgs).
+struct Workspace {
+  uint32_t max_rows;
+  uint64_t slots;           // wave slots
+  RowParams* params;        // [max_rows]
+  uint64_t* cand;           // [slots][kMaxK]
+  uint64_t* greedy;         // [slots]
+  uint32_t* spec;           // [slots] speculative stream keys
+  double* lse;              // [slots][2]
+  double* zsum;             // [slots][3]
+  uint32_t* row_done;       // [max_rows * kLineWords], zero between launches
+  uint32_t* nuc_deep;       // [max_rows]
+  float* nuc_max;           // [max_rows]
+  uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
+  Tuning tuning;            // environment overrides
+};
+
 // set_configs stages each upload in its own pinned slot and records an event
 // after the copy; a slot is rewritten only after its event, so a caller that
 // changes every row's controls on every step never waits for the stream
@@ -226,26 +246,194 @@ constexpr uint32_t kStageSlots = 8;
 struct fg_sampler_hip {
   int device;
   uint32_t vocab;
-  uint32_t max_rows;
-  RowParams* d_params;      // [max_rows]
+  Workspace ws;             // device workspace (hipMalloc'd at create)
   RowParams* h_params;      // host mirror of the uploaded table (launch-variant choice)
   RowParams* h_stage;       // pinned [kStageSlots][max_rows]: copy sources of set_configs
   hipEvent_t stage_done[kStageSlots];  // recorded after each slot's copy
   uint32_t stage_next;      // slot the next set_configs fills
   uint32_t config_rows;     // rows configured by the last set_configs
-  uint64_t slots;           // wave slots in the workspace
-  uint64_t* d_cand;         // [slots][kMaxK]
-  uint64_t* d_greedy;       // [slots]
-  uint32_t* d_spec;         // [slots] speculative stream keys
-  double* d_lse;            // [slots][2]
-  double* d_zsum;           // [slots][3]
-  uint32_t* d_row_done;     // [max_rows * kLineWords]
-  uint32_t* d_nuc_deep;     // [max_rows]
-  float* d_nuc_max;         // [max_rows]
-  Tuning tuning;            // environment overrides, read at create
-  uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
   uint64_t* counters;       // event counters, FG_SAMPLE_TRACE builds only
 };
+
+namespace {
+
+RowParams row_params(const fg_sampler_config* c) {
+  RowParams p{};
+  p.temperature = c->temperature;
+  p.top_p = c->top_p;
+  p.top_k = c->top_k;
+  p.presence = c->presence_penalty;
+  p.frequency = c->frequency_penalty;
+  p.repetition = c->repetition_penalty;
+  p.flags = fg_sampler_penalties_active(c) ? fg::kRowPenalties : 0u;
+  return p;
+}
+
+// ---- Static workspace of fg_sampler_hip_sample_static
+//
+// A file-scope device array carved into the Workspace buffers for
+// kStaticMaxRows rows.  Host code never uses the array's name as an address:
+// each device's copy is found once with hipGetSymbolAddress and that pointer
+// is used for every launch on the device.
+constexpr uint32_t kStaticMaxRows = FG_SAMPLER_HIP_STATIC_MAX_ROWS;
+constexpr uint64_t kStaticSlots = static_cast<uint64_t>(fg::kMaxGroups + kStaticMaxRows) * fg::kWaves;
+constexpr size_t align256(size_t x) { return (x + 255u) & ~static_cast<size_t>(255u); }
+constexpr size_t kOffParams = 0;
+constexpr size_t kOffCand = align256(kOffParams + sizeof(RowParams) * kStaticMaxRows);
+constexpr size_t kOffGreedy = align256(kOffCand + sizeof(uint64_t) * kStaticSlots * fg::kMaxK);
+constexpr size_t kOffSpec = align256(kOffGreedy + sizeof(uint64_t) * kStaticSlots);
+constexpr size_t kOffLse = align256(kOffSpec + sizeof(uint32_t) * kStaticSlots);
+constexpr size_t kOffZsum = align256(kOffLse + sizeof(double) * kStaticSlots * 2u);
+constexpr size_t kOffDone = align256(kOffZsum + sizeof(double) * kStaticSlots * 3u);
+constexpr size_t kOffDeep = align256(kOffDone + sizeof(uint32_t) * fg::kLineWords * kStaticMaxRows);
+constexpr size_t kOffNucMax = align256(kOffDeep + sizeof(uint32_t) * kStaticMaxRows);
+constexpr size_t kStaticBytes = align256(kOffNucMax + sizeof(float) * kStaticMaxRows);
+static_assert(kStaticBytes == FG_SAMPLER_HIP_STATIC_BYTES, "header size out of date");
+
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+constexpr int kStaticMaxDevices = 64;
+// Per device: the address of its copy of `scratch` (0 until first use).
+std::atomic<uintptr_t> g_scratch_addr[kStaticMaxDevices];
+
+hipError_t static_workspace(Workspace* w) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kStaticMaxDevices) return hipErrorInvalidDevice;
+  uintptr_t base = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!base) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!ptr) return hipErrorInvalidSymbol;
+    base = reinterpret_cast<uintptr_t>(ptr);
+    g_scratch_addr[dev].store(base, std::memory_order_release);
+  }
+  unsigned char* p = reinterpret_cast<unsigned char*>(base);
+  w->max_rows = kStaticMaxRows;
+  w->slots = kStaticSlots;
+  w->params = reinterpret_cast<RowParams*>(p + kOffParams);
+  w->cand = reinterpret_cast<uint64_t*>(p + kOffCand);
+  w->greedy = reinterpret_cast<uint64_t*>(p + kOffGreedy);
+  w->spec = reinterpret_cast<uint32_t*>(p + kOffSpec);
+  w->lse = reinterpret_cast<double*>(p + kOffLse);
+  w->zsum = reinterpret_cast<double*>(p + kOffZsum);
+  w->row_done = reinterpret_cast<uint32_t*>(p + kOffDone);
+  w->nuc_deep = reinterpret_cast<uint32_t*>(p + kOffDeep);
+  w->nuc_max = reinterpret_cast<float*>(p + kOffNucMax);
+  w->trace = nullptr;
+  w->tuning = tuning_from_env();
+  return hipSuccess;
+}
+
+// Rows of controls per launch of static_params_kernel (2 KiB of arguments).
+constexpr uint32_t kParamsPerFill = 64;
+struct StaticParams {
+  RowParams rows[kParamsPerFill];
+  uint32_t first;
+  uint32_t count;
+};
+
+// Writes rows [first, first + count) of the controls and clears their
+// arrival counters (a fill kernel, not a memset, so the call can sit in a
+// captured graph).
+__global__ void __launch_bounds__(kParamsPerFill)
+    static_params_kernel(StaticParams p, RowParams* params, uint32_t* row_done) {
+  const uint32_t t = threadIdx.x;
+  if (t < p.count) {
+    params[p.first + t] = p.rows[t];
+    row_done[static_cast<size_t>(p.first + t) * fg::kLineWords] = 0u;
+  }
+}
+
+// One fused sampling launch (two with whole-row nucleus rows) over a batch
+// whose per-row controls are h_params on the host (variant and layout choice)
+// and w.params on the device.  The caller has checked the batch against
+// w.max_rows and the configured rows.
+fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t vocab,
+                        const fg_sampler_hip_batch* b, hipStream_t stream, fg_error* err) {
+  if (!b->logits || !b->tokens || !b->uniforms || !b->rows || b->rows > w.max_rows ||
+      b->logits_stride < vocab || (b->counts && b->counts_stride < vocab) ||
+      b->logprobs > fg::kMaxK || (b->logprobs && (!b->logprob_values || !b->logprob_ids)))
+    return arg_fail(err, "invalid sampled output arguments");
+  bool same_cost = true;  // every row alike in penalties (for the paired layout)
+  bool nuc_rows = false;
+  for (uint32_t r = 0; r < b->rows; r++) {
+    same_cost &= ((h_params[r].flags ^ h_params[0].flags) & fg::kRowPenalties) == 0u;
+    nuc_rows |= h_params[r].temperature > 0.0f && h_params[r].top_k == 0u;
+  }
+  fg_sampler_hip_geometry geo;
+  plan_geometry(vocab, b->rows, nuc_rows, same_cost, w.tuning, &geo);
+  const uint32_t chunks = geo.chunks;
+  if (static_cast<uint64_t>(b->rows) * chunks * fg::kWaves > w.slots) {
+    fg_error_set(err, FG_ERR_LIMIT, "sampler workspace too small for %u rows", b->rows);
+    return FG_ERR_LIMIT;
+  }
+  fg::SampleArgs a{};
+  a.logits = b->logits;
+  a.lstride = b->logits_stride;
+  a.counts = b->counts;
+  a.cstride = b->counts_stride;
+  a.uniforms = b->uniforms;
+  a.params = w.params;
+  a.vocab = vocab;
+  a.rows = b->rows;
+  a.chunks = chunks;
+  a.wave_elems = geo.wave_elems;
+  a.wave_elems_b = geo.wave_elems_b;
+  a.split = geo.split;
+  a.pace = geo.pace;
+  a.logprobs = b->logprobs;
+  a.tokens = b->tokens;
+  a.token_logits = b->token_logits;
+  a.row_status = b->row_status;
+  a.penalised = b->penalised;
+  a.lp_values = b->logprob_values;
+  a.lp_ids = b->logprob_ids;
+  a.cand = w.cand;
+  a.greedy = w.greedy;
+  a.spec = w.spec;
+  a.lse = w.lse;
+  a.zsum = w.zsum;
+  a.row_done = w.row_done;
+  a.nuc_deep = w.nuc_deep;
+  a.nuc_max = w.nuc_max;
+  a.trace = w.trace;
+
+  // The vector path addresses a slice with 32-bit byte offsets.
+  const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
+                   a.wave_elems < (1u << 28) && a.wave_elems_b < (1u << 28) &&
+                   (!b->counts || (aligned16(b->counts) && (b->counts_stride % 4u) == 0u));
+  bool any_pen = false, any_greedy = false, any_top = b->logprobs != 0u, any_nuc = false;
+  bool any_spec = false;
+  for (uint32_t r = 0; r < b->rows; r++) {
+    const RowParams& rp = h_params[r];
+    any_pen |= (rp.flags & fg::kRowPenalties) != 0u;
+    any_greedy |= rp.temperature == 0.0f;
+    any_top |= rp.temperature > 0.0f;
+    any_nuc |= rp.temperature > 0.0f && rp.top_k == 0u;
+    any_spec |= rp.temperature > 0.0f &&
+                (rp.top_k == 0u ? fg::kMaxK : (rp.top_k > b->logprobs ? rp.top_k : b->logprobs)) >
+                    fg::kSpecMinK;
+  }
+  any_pen = any_pen && b->counts != nullptr;
+  // Speculation only runs over short slices (the kernel's own condition); a
+  // launch without it streams in shorter steps.
+  any_spec = any_spec && (a.wave_elems > a.wave_elems_b ? a.wave_elems : a.wave_elems_b) <=
+                             fg::kSpecMaxElems;
+  const int bits = (any_pen ? 1 : 0) | (any_greedy ? 2 : 0) | (any_top ? 4 : 0) |
+                   (b->logprobs ? 8 : 0) | (any_nuc ? 16 : 0) | (any_spec ? 32 : 0);
+  const uint32_t grid = b->rows * chunks;
+  (vec ? kVecLaunch[bits] : kScalarLaunch)(grid, stream, a);
+  // Whole-row nucleus rows whose cut lies past the kMaxK best are finished
+  // by a second kernel; the others return at once.
+  if (any_nuc) fg::nucleus_rows_kernel<<<b->rows, fg::kNucBlock, 0, stream>>>(a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "sampler launch");
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -514,41 +702,41 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
     return FG_ERR_OOM;
   }
   s->vocab = vocab;
-  s->max_rows = max_rows;
-  s->tuning = tuning_from_env();
+  s->ws.max_rows = max_rows;
+  s->ws.tuning = tuning_from_env();
   hipError_t e = hipGetDevice(&s->device);
   // rows * chunks(rows) <= max(target, kMaxGroups) + rows for every batch
   // size.
   const uint64_t groups_cap =
-      s->tuning.target_groups > fg::kMaxGroups ? s->tuning.target_groups : fg::kMaxGroups;
+      s->ws.tuning.target_groups > fg::kMaxGroups ? s->ws.tuning.target_groups : fg::kMaxGroups;
   const uint64_t slots = (groups_cap + max_rows) * fg::kWaves;
-  s->slots = slots;
+  s->ws.slots = slots;
   s->h_params = static_cast<RowParams*>(calloc(max_rows, sizeof(RowParams)));
   if (!s->h_params) {
     free(s);
     fg_error_set(err, FG_ERR_OOM, "allocate sampler");
     return FG_ERR_OOM;
   }
-  if (e == hipSuccess) e = hipMalloc(&s->d_params, sizeof(RowParams) * max_rows);
-  if (e == hipSuccess) e = hipMalloc(&s->d_cand, sizeof(uint64_t) * slots * fg::kMaxK);
-  if (e == hipSuccess) e = hipMalloc(&s->d_greedy, sizeof(uint64_t) * slots);
-  if (e == hipSuccess) e = hipMalloc(&s->d_spec, sizeof(uint32_t) * slots);
-  if (e == hipSuccess) e = hipMalloc(&s->d_lse, sizeof(double) * slots * 2);
-  if (e == hipSuccess) e = hipMalloc(&s->d_zsum, sizeof(double) * slots * 3);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.params, sizeof(RowParams) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.cand, sizeof(uint64_t) * slots * fg::kMaxK);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.greedy, sizeof(uint64_t) * slots);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.spec, sizeof(uint32_t) * slots);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.lse, sizeof(double) * slots * 2);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.zsum, sizeof(double) * slots * 3);
   const size_t done_bytes = sizeof(uint32_t) * fg::kLineWords * max_rows;
-  if (e == hipSuccess) e = hipMalloc(&s->d_row_done, done_bytes);
-  if (e == hipSuccess) e = hipMemset(s->d_row_done, 0, done_bytes);
-  if (e == hipSuccess) e = hipMalloc(&s->d_nuc_deep, sizeof(uint32_t) * max_rows);
-  if (e == hipSuccess) e = hipMalloc(&s->d_nuc_max, sizeof(float) * max_rows);
-  if (e == hipSuccess) e = hipMemset(s->d_params, 0, sizeof(RowParams) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.row_done, done_bytes);
+  if (e == hipSuccess) e = hipMemset(s->ws.row_done, 0, done_bytes);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.nuc_deep, sizeof(uint32_t) * max_rows);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.nuc_max, sizeof(float) * max_rows);
+  if (e == hipSuccess) e = hipMemset(s->ws.params, 0, sizeof(RowParams) * max_rows);
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&s->h_stage),
                       sizeof(RowParams) * max_rows * kStageSlots, hipHostMallocDefault);
   for (uint32_t i = 0; i < kStageSlots && e == hipSuccess; i++)
     e = hipEventCreateWithFlags(&s->stage_done[i], hipEventDisableTiming);
 #ifdef FG_SAMPLE_TRACE
-  if (e == hipSuccess) e = hipMalloc(&s->trace, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
-  if (e == hipSuccess) e = hipMemset(s->trace, 0, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
+  if (e == hipSuccess) e = hipMalloc(&s->ws.trace, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
+  if (e == hipSuccess) e = hipMemset(s->ws.trace, 0, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
   if (e == hipSuccess) e = hipMalloc(&s->counters, sizeof(uint64_t) * 16u);
   if (e == hipSuccess) e = hipMemset(s->counters, 0, sizeof(uint64_t) * 16u);
   if (e == hipSuccess)
@@ -565,16 +753,16 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
 
 void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   if (!s) return;
-  (void)hipFree(s->d_params);
-  (void)hipFree(s->d_cand);
-  (void)hipFree(s->d_greedy);
-  (void)hipFree(s->d_spec);
-  (void)hipFree(s->d_lse);
-  (void)hipFree(s->d_zsum);
-  (void)hipFree(s->d_row_done);
-  (void)hipFree(s->d_nuc_deep);
-  (void)hipFree(s->d_nuc_max);
-  (void)hipFree(s->trace);
+  (void)hipFree(s->ws.params);
+  (void)hipFree(s->ws.cand);
+  (void)hipFree(s->ws.greedy);
+  (void)hipFree(s->ws.spec);
+  (void)hipFree(s->ws.lse);
+  (void)hipFree(s->ws.zsum);
+  (void)hipFree(s->ws.row_done);
+  (void)hipFree(s->ws.nuc_deep);
+  (void)hipFree(s->ws.nuc_max);
+  (void)hipFree(s->ws.trace);
   // Pending uploads read the pinned slots: let them finish first.
   for (uint32_t i = 0; i < kStageSlots; i++) {
     if (s->stage_done[i]) {
@@ -589,7 +777,7 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
 
 fg_status fg_sampler_hip_set_configs(fg_sampler_hip* s, const fg_sampler_config* configs,
                                      uint32_t rows, uint32_t flags, void* stream, fg_error* err) {
-  if (!s || !configs || !rows || rows > s->max_rows ||
+  if (!s || !configs || !rows || rows > s->ws.max_rows ||
       (flags & ~FG_SAMPLER_HIP_ALLOW_FULL_VOCAB))
     return arg_fail(err, "invalid sampler configuration batch");
   for (uint32_t r = 0; r < rows; r++) {
@@ -599,25 +787,16 @@ fg_status fg_sampler_hip_set_configs(fg_sampler_hip* s, const fg_sampler_config*
     }
   }
   for (uint32_t r = 0; r < rows; r++) {
-    const fg_sampler_config* c = &configs[r];
-    RowParams p{};
-    p.temperature = c->temperature;
-    p.top_p = c->top_p;
-    p.top_k = c->top_k;
-    p.presence = c->presence_penalty;
-    p.frequency = c->frequency_penalty;
-    p.repetition = c->repetition_penalty;
-    p.flags = fg_sampler_penalties_active(c) ? fg::kRowPenalties : 0u;
-    s->h_params[r] = p;
+    s->h_params[r] = row_params(&configs[r]);
   }
   // The copy is ordered on `stream` after earlier launches that read
   // d_params and before later ones; only its pinned source needs guarding.
   const uint32_t slot = s->stage_next;
-  RowParams* src = s->h_stage + static_cast<size_t>(slot) * s->max_rows;
+  RowParams* src = s->h_stage + static_cast<size_t>(slot) * s->ws.max_rows;
   hipError_t e = hipEventSynchronize(s->stage_done[slot]);
   if (e == hipSuccess) {
     memcpy(src, s->h_params, sizeof(RowParams) * rows);
-    e = hipMemcpyAsync(s->d_params, src, sizeof(RowParams) * rows, hipMemcpyHostToDevice,
+    e = hipMemcpyAsync(s->ws.params, src, sizeof(RowParams) * rows, hipMemcpyHostToDevice,
                        as_stream(stream));
   }
   if (e == hipSuccess) e = hipEventRecord(s->stage_done[slot], as_stream(stream));
@@ -629,87 +808,44 @@ fg_status fg_sampler_hip_set_configs(fg_sampler_hip* s, const fg_sampler_config*
 
 fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b, void* stream,
                                 fg_error* err) {
-  if (!s || !b) return arg_fail(err, "invalid sampled output arguments");
-  if (!b->logits || !b->tokens || !b->uniforms || !b->rows || b->rows > s->max_rows ||
-      b->rows > s->config_rows || b->logits_stride < s->vocab ||
-      (b->counts && b->counts_stride < s->vocab) || b->logprobs > fg::kMaxK ||
-      (b->logprobs && (!b->logprob_values || !b->logprob_ids)))
+  if (!s || !b || b->rows > s->config_rows)
     return arg_fail(err, "invalid sampled output arguments");
-  const uint32_t vocab = s->vocab;
-  bool same_cost = true;  // every row alike in penalties (for the paired layout)
-  bool nuc_rows = false;
-  for (uint32_t r = 0; r < b->rows; r++) {
-    same_cost &= ((s->h_params[r].flags ^ s->h_params[0].flags) & fg::kRowPenalties) == 0u;
-    nuc_rows |= s->h_params[r].temperature > 0.0f && s->h_params[r].top_k == 0u;
-  }
-  fg_sampler_hip_geometry geo;
-  plan_geometry(vocab, b->rows, nuc_rows, same_cost, s->tuning, &geo);
-  const uint32_t chunks = geo.chunks;
-  if (static_cast<uint64_t>(b->rows) * chunks * fg::kWaves > s->slots) {
-    fg_error_set(err, FG_ERR_LIMIT, "sampler workspace too small for %u rows", b->rows);
+  return sample_launch(s->ws, s->h_params, s->vocab, b, as_stream(stream), err);
+}
+
+fg_status fg_sampler_hip_sample_static(uint32_t vocab, const fg_sampler_config* configs,
+                                       uint32_t flags, const fg_sampler_hip_batch* b,
+                                       void* stream, fg_error* err) {
+  if (!configs || !b || !vocab || vocab >= 0x80000000u || !b->rows ||
+      (flags & ~FG_SAMPLER_HIP_ALLOW_FULL_VOCAB))
+    return arg_fail(err, "invalid sampled output arguments");
+  if (b->rows > kStaticMaxRows) {
+    fg_error_set(err, FG_ERR_LIMIT, "%u rows exceed the static sampler workspace (%u rows)",
+                 b->rows, kStaticMaxRows);
     return FG_ERR_LIMIT;
   }
-  fg::SampleArgs a{};
-  a.logits = b->logits;
-  a.lstride = b->logits_stride;
-  a.counts = b->counts;
-  a.cstride = b->counts_stride;
-  a.uniforms = b->uniforms;
-  a.params = s->d_params;
-  a.vocab = vocab;
-  a.rows = b->rows;
-  a.chunks = chunks;
-  a.wave_elems = geo.wave_elems;
-  a.wave_elems_b = geo.wave_elems_b;
-  a.split = geo.split;
-  a.pace = geo.pace;
-  a.logprobs = b->logprobs;
-  a.tokens = b->tokens;
-  a.token_logits = b->token_logits;
-  a.row_status = b->row_status;
-  a.penalised = b->penalised;
-  a.lp_values = b->logprob_values;
-  a.lp_ids = b->logprob_ids;
-  a.cand = s->d_cand;
-  a.greedy = s->d_greedy;
-  a.spec = s->d_spec;
-  a.lse = s->d_lse;
-  a.zsum = s->d_zsum;
-  a.row_done = s->d_row_done;
-  a.nuc_deep = s->d_nuc_deep;
-  a.nuc_max = s->d_nuc_max;
-  a.trace = s->trace;
-
-  // The vector path addresses a slice with 32-bit byte offsets.
-  const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
-                   a.wave_elems < (1u << 28) && a.wave_elems_b < (1u << 28) &&
-                   (!b->counts || (aligned16(b->counts) && (b->counts_stride % 4u) == 0u));
-  bool any_pen = false, any_greedy = false, any_top = b->logprobs != 0u, any_nuc = false;
-  bool any_spec = false;
+  RowParams h[kStaticMaxRows];
   for (uint32_t r = 0; r < b->rows; r++) {
-    const RowParams& rp = s->h_params[r];
-    any_pen |= (rp.flags & fg::kRowPenalties) != 0u;
-    any_greedy |= rp.temperature == 0.0f;
-    any_top |= rp.temperature > 0.0f;
-    any_nuc |= rp.temperature > 0.0f && rp.top_k == 0u;
-    any_spec |= rp.temperature > 0.0f &&
-                (rp.top_k == 0u ? fg::kMaxK : (rp.top_k > b->logprobs ? rp.top_k : b->logprobs)) >
-                    fg::kSpecMinK;
+    if (!config_ok(&configs[r], flags)) {
+      fg_error_set(err, FG_ERR_ARGUMENT, "invalid sampler controls (row %u)", r);
+      return FG_ERR_ARGUMENT;
+    }
+    h[r] = row_params(&configs[r]);
   }
-  any_pen = any_pen && b->counts != nullptr;
-  // Speculation only runs over short slices (the kernel's own condition); a
-  // launch without it streams in shorter steps.
-  any_spec = any_spec && (a.wave_elems > a.wave_elems_b ? a.wave_elems : a.wave_elems_b) <=
-                             fg::kSpecMaxElems;
-  const int bits = (any_pen ? 1 : 0) | (any_greedy ? 2 : 0) | (any_top ? 4 : 0) |
-                   (b->logprobs ? 8 : 0) | (any_nuc ? 16 : 0) | (any_spec ? 32 : 0);
-  const uint32_t grid = b->rows * chunks;
-  (vec ? kVecLaunch[bits] : kScalarLaunch)(grid, as_stream(stream), a);
-  // Whole-row nucleus rows whose cut lies past the kMaxK best are finished
-  // by a second kernel; the others return at once.
-  if (any_nuc) fg::nucleus_rows_kernel<<<b->rows, fg::kNucBlock, 0, as_stream(stream)>>>(a);
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? FG_OK : hip_fail(err, e, "sampler launch");
+  Workspace w;
+  hipError_t e = static_workspace(&w);
+  if (e != hipSuccess) return hip_fail(err, e, "static sampler workspace");
+  // Controls and cleared row counters, by value through kernel arguments.
+  for (uint32_t first = 0; first < b->rows; first += kParamsPerFill) {
+    StaticParams p;
+    p.first = first;
+    p.count = b->rows - first < kParamsPerFill ? b->rows - first : kParamsPerFill;
+    memcpy(p.rows, h + first, sizeof(RowParams) * p.count);
+    static_params_kernel<<<1, kParamsPerFill, 0, as_stream(stream)>>>(p, w.params, w.row_done);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(err, e, "static sampler controls");
+  return sample_launch(w, h, vocab, b, as_stream(stream), err);
 }
 
 fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
@@ -720,7 +856,7 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
     return arg_fail(err, "invalid output history token");
   fg::history_increment_kernel<<<(rows + 255u) / 256u, 256, 0, as_stream(stream)>>>(
       counts, counts_stride, s->vocab, tokens, row_status,
-      reinterpret_cast<const uint32_t*>(s->d_params) + offsetof(RowParams, flags) / 4u,
+      reinterpret_cast<const uint32_t*>(s->ws.params) + offsetof(RowParams, flags) / 4u,
       sizeof(RowParams) / 4u, rows);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "history increment launch");
@@ -729,7 +865,7 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
 #ifdef FG_SAMPLE_TRACE
 // Copies the last launch's phase timestamps ([workgroup][8]) to the host.
 fg_status fg_sampler_hip_trace_copy(fg_sampler_hip* s, uint64_t* host, uint64_t count) {
-  const hipError_t e = hipMemcpy(host, s->trace, sizeof(uint64_t) * count, hipMemcpyDeviceToHost);
+  const hipError_t e = hipMemcpy(host, s->ws.trace, sizeof(uint64_t) * count, hipMemcpyDeviceToHost);
   return e == hipSuccess ? FG_OK : FG_ERR_UNAVAILABLE;
 }
 // Copies the event counters (16 u64) to the host and clears them.

@@ -40,7 +40,7 @@ EXPORTS = (
     "fg_output_history_encode", "fg_output_history_encode_vocab",
     "fg_output_history_decode", "fg_output_history_decode_vocab",
     "fg_sampler_hip_create", "fg_sampler_hip_destroy", "fg_sampler_hip_set_configs",
-    "fg_sampler_hip_sample", "fg_sampler_hip_history_increment",
+    "fg_sampler_hip_sample", "fg_sampler_hip_history_increment", "fg_sampler_hip_sample_static",
     "fg_output_better", "fg_output_combine", "fg_output_split_way_for_rank",
     "fg_output_split_rank", "fg_output_split_span", "fg_output_split_combine_finalists",
     "fg_hip_output_slice_create", "fg_hip_output_slice_destroy", "fg_hip_output_slice_ways",
@@ -155,6 +155,8 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_sampler_hip_destroy": (None, [P]),
         "fg_sampler_hip_set_configs": (C.c_int, [P, C.POINTER(SamplerConfig), u32, u32, P, E]),
         "fg_sampler_hip_sample": (C.c_int, [P, C.POINTER(Batch), P, E]),
+        "fg_sampler_hip_sample_static":
+            (C.c_int, [u32, C.POINTER(SamplerConfig), u32, C.POINTER(Batch), P, E]),
         "fg_sampler_hip_history_increment": (C.c_int, [P, P, u64, P, P, u32, P, E]),
         "fg_output_better": (C.c_bool, [f32, u32, f32, u32]),
         "fg_output_combine": (None, [f32, u32, f32, u32, C.POINTER(f32), C.POINTER(u32)]),
@@ -469,6 +471,31 @@ class HipSampler:
         _check(self._lib.fg_sampler_hip_history_increment(
             self.handle, _ptr(counts), counts.stride(0), _ptr(tokens), _ptr(row_status), rows,
             _stream(stream), C.byref(err)), err)
+
+
+STATIC_MAX_ROWS = 256
+
+
+def sample_static(vocab, configs, logits, uniforms, tokens, counts=None, token_logits=None,
+                  row_status=None, penalised=None, logprobs=0, logprob_values=None,
+                  logprob_ids=None, flags=0, rows=None, logits_stride=None, counts_stride=None,
+                  stream=None):
+    """fg_sampler_hip_sample_static: configs + sample in one call, no sampler
+    object, workspace in the library's static device array (allocates
+    nothing)."""
+    rows = rows if rows is not None else logits.shape[0]
+    if len(configs) < rows:
+        raise ValueError(f"{len(configs)} configs for {rows} rows")
+    arr = (SamplerConfig * len(configs))(*configs)
+    b = Batch(
+        _ptr(logits), logits_stride if logits_stride is not None else logits.stride(0),
+        _ptr(counts), (counts_stride if counts_stride is not None
+                       else (counts.stride(0) if counts is not None else 0)),
+        _ptr(uniforms), rows, _ptr(tokens), _ptr(token_logits), _ptr(row_status),
+        _ptr(penalised), logprobs, _ptr(logprob_values), _ptr(logprob_ids))
+    err = FgError()
+    _check(lib().fg_sampler_hip_sample_static(vocab, arr, flags, C.byref(b), _stream(stream),
+                                              C.byref(err)), err)
 
 
 def plan(vocab: int, rows: int, traits: int = 0) -> Geometry:

@@ -186,6 +186,24 @@ typedef struct fg_sampler_hip_batch {
 fg_status fg_sampler_hip_sample(fg_sampler_hip *sampler, const fg_sampler_hip_batch *batch,
                                 void *stream, fg_error *err);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  fg_sampler_hip_set_configs + fg_sampler_hip_sample in
+ * one call, with no sampler object: the same kernels and the same results,
+ * but the controls travel as kernel arguments and the workspace is a
+ * file-scope device array of FG_SAMPLER_HIP_STATIC_BYTES bytes per GPU
+ * (allocated when the library loads, held until the process ends).  Allocates
+ * nothing and never waits for the device.  configs[r] are row r's controls
+ * (host memory, read before return); flags as for set_configs.  At most
+ * FG_SAMPLER_HIP_STATIC_MAX_ROWS rows (more: FG_ERR_LIMIT).  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (different
+ * streams, or another thread) race and must be serialised by the caller. */
+#define FG_SAMPLER_HIP_STATIC_MAX_ROWS 256u
+#define FG_SAMPLER_HIP_STATIC_BYTES 2930688u
+fg_status fg_sampler_hip_sample_static(uint32_t vocab, const fg_sampler_config *configs,
+                                       uint32_t flags, const fg_sampler_hip_batch *batch,
+                                       void *stream, fg_error *err);
+
 /* Launch geometry of fg_sampler_hip_sample, for tests and tuning (no
  * counterpart in the reference, whose per-tile dispatches have a fixed
  * shape, shaders/fg_topk_select.comp).  Each row is split into `chunks`
