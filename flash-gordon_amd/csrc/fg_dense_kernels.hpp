@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kDenseBlock) void dense_q8_finalist_kernel(DenseArg
       const uint32_t tok = a.token0 + t;
       __hip_atomic_fetch_max(a.keys + tok, static_cast<unsigned long long>(m), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
-      wait_memory();
+      wait_memory();  // hand-off ordering: see wait_memory()
       const uint32_t arrived =
           __hip_atomic_fetch_add(a.arrivals + tok, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = arrived + 1u == gridDim.x;

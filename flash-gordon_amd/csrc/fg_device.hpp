@@ -337,6 +337,26 @@ __device__ __forceinline__ void wave_merge_desc2(uint64_t& a0, uint64_t b0, uint
 
 // Waits until this wave's memory operations have completed; the signal
 // fences keep the compiler from moving memory operations across the wait.
+//
+// Cross-workgroup hand-offs (publish, count in, the last one reads) use it
+// instead of release/acquire fences.  In the HIP memory model a relaxed
+// counter increment is ordered after earlier stores only by a release, and
+// the reader's loads after it only by an acquire; at agent scope on gfx950
+// those are an L2 write-back (buffer_wbl2) and an L2 invalidate (buffer_inv),
+// which took a sampling launch from 20 us to 135 us.  The hand-offs get the
+// same ordering from what the ISA guarantees for the accesses they use:
+//  1. every published value is an agent-scope atomic store (sc1), written
+//     through to the device-coherent level, never left dirty in one XCD's L2
+//     (the write-back a release adds is for plain stores, and there are none);
+//  2. s_waitcnt 0 returns only when those stores are acknowledged by that
+//     level, and only then is the counter's agent-scope atomic issued;
+//  3. the reader branches on the atomic's returned value before it issues
+//     its loads, and those are agent-scope atomic loads (sc1), which do not
+//     return a stale copy from its own caches (the invalidate an acquire adds
+//     is for plain loads, and there are none).
+// So a workgroup that learns from the counter that it is last reads every
+// partial published before the others counted in.  The signal fences keep
+// the compiler from moving the stores past the wait.
 __device__ __forceinline__ void wait_memory() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);

@@ -94,7 +94,7 @@ struct SampleArgs {
                          // reset by the last workgroup
   uint32_t* nuc_deep;    // [rows] whole-row nucleus: 1 = cut deeper than the kMaxK best
   float* nuc_max;        // [rows] whole-row nucleus: the row's largest finite value
-  uint64_t* trace;       // FG_SAMPLE_TRACE builds only: [workgroup][8] timestamps
+  uint64_t* trace;       // FG_SAMPLE_TRACE builds only: [workgroup][16] timestamps
 };
 
 // Phase timestamps (s_memrealtime, 100 MHz) for builds with FG_SAMPLE_TRACE;
@@ -103,19 +103,23 @@ struct SampleArgs {
 #define FG_TRACE(a, slot)                                                          \
   do {                                                                             \
     if (threadIdx.x == 0 && (a).trace)                                             \
-      (a).trace[static_cast<uint64_t>(blockIdx.x) * 8u + (slot)] =                 \
+      (a).trace[static_cast<uint64_t>(blockIdx.x) * 16u + (slot)] =                \
           __builtin_amdgcn_s_memrealtime();                                        \
   } while (0)
-// Event counters of FG_SAMPLE_TRACE builds: trace[8 * groups + i].
+// Event counters of FG_SAMPLE_TRACE builds (FG_SAMPLE_COUNT also set; they
+// slow the launch down): g_trace_counters[i].
 __device__ uint64_t* g_trace_counters;
+#else
+#define FG_TRACE(a, slot) \
+  do {                    \
+  } while (0)
+#endif
+#if defined(FG_SAMPLE_TRACE) && defined(FG_SAMPLE_COUNT)
 #define FG_COUNT(i, v)                                                             \
   do {                                                                             \
     if (g_trace_counters && lane_id() == 0) atomicAdd(&g_trace_counters[i], (v));  \
   } while (0)
 #else
-#define FG_TRACE(a, slot) \
-  do {                    \
-  } while (0)
 #define FG_COUNT(i, v) \
   do {                 \
   } while (0)
@@ -201,6 +205,24 @@ __device__ __forceinline__ uint64_t staged_comp(uint64_t x) {
                        : x;
 }
 
+// Drops the staged entries that no longer beat R, keeping the rest in
+// order at the front of the stage (a chunk is read before anything is
+// written over it).
+__device__ __forceinline__ void top_compact(TopList& t) {
+  const uint32_t lane = lane_id();
+  uint32_t w = 0u;
+  for (uint32_t c = 0; c < t.n; c += kWave) {
+    const uint64_t x = c + lane < t.n ? staged_comp(t.buf[c + lane]) : 0ull;
+    wave_lds_sync();
+    const bool keep = x > t.R;
+    const uint64_t m = ballot(keep);
+    if (keep) t.buf[w + lanes_below(m)] = x;
+    w += static_cast<uint32_t>(__popcll(m));
+    wave_lds_sync();
+  }
+  t.n = w;
+}
+
 // Raises the filter from the staged entries alone and drops those it beats,
 // without sorting: the kk-th largest of the lanes' maximum staged keys (a
 // ballot radix search, to 2^12 key units) has at least kk staged entries at
@@ -223,18 +245,7 @@ __device__ __forceinline__ void top_select(TopList& t) {
     top_raise(t, key_floor(T));
     top_share(t, T);
   }
-  // Compact in place: a chunk is read before anything is written over it.
-  uint32_t w = 0u;
-  for (uint32_t c = 0; c < t.n; c += kWave) {
-    uint64_t x = c + lane < t.n ? staged_comp(t.buf[c + lane]) : 0ull;
-    wave_lds_sync();
-    const bool keep = x > t.R;
-    const uint64_t m = ballot(keep);
-    if (keep) t.buf[w + lanes_below(m)] = x;
-    w += static_cast<uint32_t>(__popcll(m));
-    wave_lds_sync();
-  }
-  t.n = w;
+  top_compact(t);
 }
 
 // Moves staged entries into the list: whole groups of 64, or everything when
@@ -1139,7 +1150,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
         store_coherent_f64(a.zsum + slot * 3 + 2, zs.e);
       }
     }
-    wait_memory();
+    wait_memory();  // hand-off ordering: see wait_memory()
     FG_TRACE(a, 3);
     uint32_t arrived = 0u;
     if (lane == 0) arrived = atomicAdd(&a.row_done[row * kLineWords], 1u);

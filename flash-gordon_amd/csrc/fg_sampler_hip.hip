@@ -735,8 +735,8 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   for (uint32_t i = 0; i < kStageSlots && e == hipSuccess; i++)
     e = hipEventCreateWithFlags(&s->stage_done[i], hipEventDisableTiming);
 #ifdef FG_SAMPLE_TRACE
-  if (e == hipSuccess) e = hipMalloc(&s->ws.trace, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
-  if (e == hipSuccess) e = hipMemset(s->ws.trace, 0, sizeof(uint64_t) * 8u * (groups_cap + max_rows));
+  if (e == hipSuccess) e = hipMalloc(&s->ws.trace, sizeof(uint64_t) * 16u * (groups_cap + max_rows));
+  if (e == hipSuccess) e = hipMemset(s->ws.trace, 0, sizeof(uint64_t) * 16u * (groups_cap + max_rows));
   if (e == hipSuccess) e = hipMalloc(&s->counters, sizeof(uint64_t) * 16u);
   if (e == hipSuccess) e = hipMemset(s->counters, 0, sizeof(uint64_t) * 16u);
   if (e == hipSuccess)

@@ -87,7 +87,7 @@ __global__ __launch_bounds__(kSliceBlock) void slice_finalist_kernel(
   // and invalidate an acquire-release fence would cost every workgroup.
   __hip_atomic_fetch_max(keys + row, static_cast<unsigned long long>(best), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
-  wait_memory();
+  wait_memory();  // hand-off ordering: see wait_memory()
   const uint32_t arrived =
       __hip_atomic_fetch_add(arrivals + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (arrived + 1u != gridDim.x) return;
