@@ -62,14 +62,14 @@ class cfg(dict):
         self.c = fg_hip.make_config(t, p, k, presence=pres, frequency=freq, repetition=rep)
 
 
-def zipf_counts(torch, g, dev, rows, draws, perm):
+def zipf_counts(torch, g, dev, rows, draws, perm, vocab=VOCAB):
     """Per-row u32 counts of `draws` Zipf(1.1) token ids (rank -> id by a
     permutation), as the configs' history tables."""
-    ranks = torch.arange(1, VOCAB + 1, device=dev, dtype=torch.float64)
+    ranks = torch.arange(1, vocab + 1, device=dev, dtype=torch.float64)
     zipf = ranks.pow(-1.1)
     zipf = (zipf / zipf.sum()).float()
-    hist = perm[torch.multinomial(zipf.expand(rows, VOCAB), draws, replacement=True, generator=g)]
-    c = torch.zeros((rows, VOCAB), dtype=torch.int32, device=dev)
+    hist = perm[torch.multinomial(zipf.expand(rows, vocab), draws, replacement=True, generator=g)]
+    c = torch.zeros((rows, vocab), dtype=torch.int32, device=dev)
     c.scatter_add_(1, hist, torch.ones_like(hist, dtype=torch.int32))
     return c
 
@@ -238,11 +238,20 @@ def lm_head_bench(args, torch, fg_hip, dev):
     status = torch.empty(tokens, dtype=torch.int32, device=dev)
     logits = torch.empty(tokens * LM_VOCAB, device=dev)
     stream = torch.cuda.current_stream()
+    if args.sampled:
+        # Config 2's controls and history statistics at the LM head's vocabulary.
+        ctl = [fg_hip.make_config(0.7, 0.8, 20, presence=1.5, repetition=1.05)] * tokens
+        perm = torch.randperm(LM_VOCAB, generator=g, device=dev)
+        counts = zipf_counts(torch, g, dev, tokens, 1024, perm, vocab=LM_VOCAB)
+        uniforms = torch.rand(tokens, generator=g, device=dev)
 
     def step():
         if args.unfused:
             fg_hip.dense_q8_0_cooked(logits, w, x, LM_WIDTH, LM_VOCAB, tokens,
                                      stream=stream.cuda_stream)
+        elif args.sampled:
+            sl.run_dense_sampled(w, x, LM_WIDTH, tokens, ctl, uniforms, ids, vals, status,
+                                 counts=counts, stream=stream.cuda_stream)
         else:
             sl.run_dense(w, x, LM_WIDTH, tokens, vals, ids, status, stream=stream.cuda_stream)
 
@@ -259,22 +268,39 @@ def lm_head_bench(args, torch, fg_hip, dev):
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end)
     per_s = ms / 1e3 / args.steps
-    if not args.unfused:
+    if args.sampled:
+        # The same tokens from the unfused path: plain product, then the sampler.
+        fg_hip.dense_q8_0_cooked(logits, w, x, LM_WIDTH, LM_VOCAB, tokens, stream=stream.cuda_stream)
+        smp = fg_hip.HipSampler(LM_VOCAB, tokens)
+        smp.set_configs(ctl, stream=stream.cuda_stream)
+        want = torch.empty(tokens, dtype=torch.int32, device=dev)
+        smp.sample(logits.view(tokens, LM_VOCAB), uniforms, want, counts=counts,
+                   stream=stream.cuda_stream)
+        torch.cuda.synchronize()
+        assert bool((ids == want).all()), "fused sampled tokens differ from the unfused path"
+        assert int(status.abs().sum()) == 0
+    elif not args.unfused:
         fg_hip.dense_q8_0_cooked(logits, w, x, LM_WIDTH, LM_VOCAB, tokens, stream=stream.cuda_stream)
         y = logits.view(tokens, LM_VOCAB)
         torch.cuda.synchronize()
         assert bool((ids.to(torch.int64) == torch.argmax(y, dim=1)).all()), "finalist != argmax"
         assert int(status.abs().sum()) == 0
-    alg = nbytes + 4 * LM_WIDTH * tokens + (4 * LM_VOCAB * tokens if args.unfused else 0)
-    kernel = "fg::dense_q8_cooked_kernel" if args.unfused else "fg::dense_q8_finalist_kernel"
+    # Algorithmic bytes: the weights and inputs once, the logits written when
+    # unfused, the history counts read when sampled.
+    alg = (nbytes + 4 * LM_WIDTH * tokens + (4 * LM_VOCAB * tokens if args.unfused else 0)
+           + (4 * LM_VOCAB * tokens if args.sampled else 0))
+    kernel = ("fg::dense_q8_cooked_kernel" if args.unfused else
+              "fg::dense_q8_sample_kernel" if args.sampled else "fg::dense_q8_finalist_kernel")
+    what = ("logits" if args.unfused else
+            "fused penalties + top-k 20 + top-p 0.8 + draw" if args.sampled else
+            "fused greedy finalist")
     print(json.dumps({
-        "metric": f"LM-head tokens/sec (Q8_0 {LM_VOCAB} x {LM_WIDTH}, "
-                  f"{'logits' if args.unfused else 'fused greedy finalist'})",
+        "metric": f"LM-head tokens/sec (Q8_0 {LM_VOCAB} x {LM_WIDTH}, {what})",
         "value": round(tokens / per_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "q8_0 x f32",
         "data": "synthetic (random Q8_0 bytes, binary16 scales in [1e-3, 2e-2], N(0,1) hidden)",
-        "config": {"workload": f"lm-head-{'plain' if args.unfused else 'finalist'}-t{tokens}",
+        "config": {"workload": f"lm-head-{'plain' if args.unfused else 'sampled' if args.sampled else 'finalist'}-t{tokens}",
                    "rows": LM_VOCAB, "width": LM_WIDTH, "tokens": tokens,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(alg / per_s / 1e9, 1), "peak": HBM_PEAK_GBS,
@@ -486,6 +512,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=1, help="--lm-head: hidden vectors per step")
     ap.add_argument("--unfused", action="store_true",
                     help="--lm-head: the plain product writing logits (no finalist)")
+    ap.add_argument("--sampled", action="store_true",
+                    help="--lm-head: fused with config 2's penalties, top-k, top-p and draw")
     ap.add_argument("--history", action="store_true",
                     help="time the history count tables rebuilt from wire payloads")
     ap.add_argument("--topk-reduce", action="store_true",

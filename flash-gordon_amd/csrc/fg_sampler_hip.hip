@@ -10,6 +10,7 @@
 
 #include "fg_sampler_hip.h"
 #include "fg_dense_kernels.hpp"
+#include "fg_lmhead_sample_kernels.hpp"
 #include "fg_nucleus_kernels.hpp"
 #include "fg_sample_kernels.hpp"
 #include "fg_split_kernels.hpp"
@@ -510,6 +511,14 @@ struct fg_hip_output_slice {
   uint32_t vocab, ways, first_row, rows, max_batch;
   unsigned long long* d_keys;  // per batch row; zero between calls
   uint32_t* d_arrivals;        // per batch row; zero between calls
+  // Sampled LM-head workspace (fg::LmSampleArgs), for whole-head slices.
+  uint32_t wg_cap, grp_cap;
+  uint64_t* d_wg_lists;
+  uint32_t* d_wg_count;
+  uint32_t* d_lm_lines;      // counters, a 128-byte line each; zero between calls
+  uint64_t* d_grp_lists;
+  uint32_t* d_grp_count;
+  fg::LmWork* d_lmwork;         // the pointers above, for the kernel
 };
 
 fg_status fg_hip_output_slice_create(fg_hip_output_slice** out, uint32_t vocab, uint32_t ways,
@@ -525,11 +534,49 @@ fg_status fg_hip_output_slice_create(fg_hip_output_slice** out, uint32_t vocab, 
     fg_error_set(err, FG_ERR_OOM, "output slice");
     return FG_ERR_OOM;
   }
-  *s = {vocab, ways, first_row, rows, max_batch_rows, nullptr, nullptr};
+  s->vocab = vocab;
+  s->ways = ways;
+  s->first_row = first_row;
+  s->rows = rows;
+  s->max_batch = max_batch_rows;
   hipError_t e = hipMalloc(&s->d_keys, sizeof(unsigned long long) * max_batch_rows);
   if (e == hipSuccess) e = hipMalloc(&s->d_arrivals, sizeof(uint32_t) * max_batch_rows);
   if (e == hipSuccess) e = hipMemset(s->d_keys, 0, sizeof(unsigned long long) * max_batch_rows);
   if (e == hipSuccess) e = hipMemset(s->d_arrivals, 0, sizeof(uint32_t) * max_batch_rows);
+  if (ways == 1u) {
+    // Two tokens per pass: lists of every workgroup and every group.
+    s->wg_cap = dense_groups(rows);
+    s->grp_cap = (s->wg_cap + fg::kLmGroup - 1u) / fg::kLmGroup;
+    const size_t wl = sizeof(uint64_t) * 2u * s->wg_cap * fg::kMaxK;
+    if (e == hipSuccess) e = hipMalloc(&s->d_wg_lists, wl);
+    if (e == hipSuccess) e = hipMalloc(&s->d_wg_count, sizeof(uint32_t) * 2u * s->wg_cap);
+    // Counters and running values, one 128-byte line each, then the running
+    // lists (zero between calls).
+    const size_t line = sizeof(uint32_t) * fg::kLineWords;
+    const size_t lines = line * 2u * (4u + s->grp_cap);
+    if (e == hipSuccess)
+      e = hipMalloc(&s->d_grp_lists, sizeof(uint64_t) * 2u * s->grp_cap * fg::kMaxK);
+    if (e == hipSuccess) e = hipMalloc(&s->d_grp_count, sizeof(uint32_t) * 2u * s->grp_cap);
+    if (e == hipSuccess) e = hipMalloc(&s->d_lm_lines, lines);
+    if (e == hipSuccess) e = hipMemset(s->d_lm_lines, 0, lines);
+    uint8_t* base = reinterpret_cast<uint8_t*>(s->d_lm_lines);
+    fg::LmWork w{};
+    w.vocab = vocab;
+    w.wg_cap = s->wg_cap;
+    w.grp_cap = s->grp_cap;
+    w.keys = reinterpret_cast<unsigned long long*>(base);
+    w.arrivals = reinterpret_cast<uint32_t*>(base + 2u * line);
+    w.bound = reinterpret_cast<unsigned long long*>(base + 4u * line);
+    w.fin_arrivals = reinterpret_cast<uint32_t*>(base + 6u * line);
+    w.grp_arrivals = reinterpret_cast<uint32_t*>(base + 8u * line);
+    w.grp_lists = s->d_grp_lists;
+    w.grp_count = s->d_grp_count;
+    w.wg_lists = s->d_wg_lists;
+    w.wg_count = s->d_wg_count;
+    if (e == hipSuccess) e = hipMalloc(&s->d_lmwork, sizeof w);
+    if (e == hipSuccess) e = hipMemcpy(s->d_lmwork, &w, sizeof w, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+  }
   if (e != hipSuccess) {
     fg_hip_output_slice_destroy(s);
     return hip_fail(err, e, "output slice workspace");
@@ -542,6 +589,12 @@ void fg_hip_output_slice_destroy(fg_hip_output_slice* s) {
   if (!s) return;
   (void)hipFree(s->d_keys);
   (void)hipFree(s->d_arrivals);
+  (void)hipFree(s->d_wg_lists);
+  (void)hipFree(s->d_wg_count);
+  (void)hipFree(s->d_lm_lines);
+  (void)hipFree(s->d_grp_lists);
+  (void)hipFree(s->d_grp_count);
+  (void)hipFree(s->d_lmwork);
   free(s);
 }
 
@@ -607,6 +660,58 @@ fg_status fg_hip_output_slice_run_dense(fg_hip_output_slice* s, const void* weig
   a.status = row_status;
   const hipError_t e = dense_launch<true>(a, tokens, as_stream(stream));
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "output slice dense launch");
+}
+
+fg_status fg_hip_output_slice_run_dense_sampled(
+    fg_hip_output_slice* s, const void* weights, const float* hidden, uint32_t in,
+    uint32_t tokens, float scale, const fg_sampler_config* configs, const uint32_t* counts,
+    uint64_t counts_stride, const float* uniforms, uint32_t* out_tokens, float* out_logits,
+    int32_t* row_status, void* stream, fg_error* err) {
+  fg::LmSampleArgs a{};
+  if (!s || s->ways != 1u || s->first_row != 0u || s->rows != s->vocab || !weights || !hidden ||
+      !configs || !uniforms || !out_tokens || !out_logits || !row_status || !tokens ||
+      tokens > s->max_batch || (counts && counts_stride < s->vocab) ||
+      !dense_geometry(in, s->rows, &a.d) || !aligned16(weights) || !aligned16(hidden))
+    return arg_fail(err, "invalid sampled output arguments");
+  for (uint32_t t = 0; t < tokens; t++) {
+    // src/sampler.c:24-38: 1 <= top_k <= 64, which the candidate lists need.
+    if (!config_ok(&configs[t], 0u)) {
+      fg_error_set(err, FG_ERR_ARGUMENT, "invalid sampler controls (token %u)", t);
+      return FG_ERR_ARGUMENT;
+    }
+  }
+  a.d.w = static_cast<const uint8_t*>(weights);
+  a.d.x = hidden;
+  a.d.y = nullptr;
+  a.d.scale = scale;
+  a.d.first_row = 0u;
+  a.d.values = out_logits;
+  a.d.ids = out_tokens;
+  a.d.status = row_status;
+  a.counts = counts;
+  a.cstride = counts_stride;
+  a.uniforms = uniforms;
+  a.work = s->d_lmwork;
+  const uint32_t groups = dense_groups(s->rows);
+  hipStream_t st = as_stream(stream);
+  for (uint32_t t0 = 0; t0 < tokens; t0 += kDensePassTokens) {
+    a.d.token0 = t0;
+    a.d.tokens = tokens - t0 < kDensePassTokens ? tokens - t0 : kDensePassTokens;
+    for (uint32_t t = 0; t < 2u; t++)
+      a.p[t] = t < a.d.tokens ? row_params(&configs[t0 + t]) : RowParams{};
+    // The merges reuse the staged inputs' LDS: at least one TopList stage.
+    const size_t merge = sizeof(uint64_t) * (fg::kCap + fg::kWave);
+    if (a.d.tokens == 1u) {
+      const size_t lds = sizeof(float) * a.d.in > merge ? sizeof(float) * a.d.in : merge;
+      fg::dense_q8_sample_kernel<1><<<groups, fg::kDenseBlock, lds, st>>>(a);
+    } else {
+      const size_t lds = sizeof(float) * a.d.in * 2u > merge ? sizeof(float) * a.d.in * 2u : merge;
+      fg::dense_q8_sample_kernel<2><<<groups, fg::kDenseBlock, lds, st>>>(a);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(err, e, "sampled output launch");
+  }
+  return FG_OK;
 }
 
 fg_status fg_hip_output_split_combine(uint32_t* tokens, float* logits_out, int32_t* row_status,
@@ -861,6 +966,14 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "history increment launch");
 }
+
+#ifdef FG_LM_TRACE
+// Copies the sampled LM head's phase timestamps ([workgroup][8]) to the host.
+fg_status fg_lm_trace_copy(uint64_t* host, uint64_t count) {
+  const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(fg::g_lm_trace), sizeof(uint64_t) * count);
+  return e == hipSuccess ? FG_OK : FG_ERR_UNAVAILABLE;
+}
+#endif
 
 #ifdef FG_SAMPLE_TRACE
 // Copies the last launch's phase timestamps ([workgroup][8]) to the host.

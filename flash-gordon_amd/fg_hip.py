@@ -48,6 +48,7 @@ EXPORTS = (
     "fg_f16_to_f32", "fg_f32_to_f16", "fg_quantize_q8_0", "fg_dequantize_q8_0",
     "fg_q8_0_cooked_tile_bytes", "fg_q8_0_cooked_matrix_bytes", "fg_cook_q8_0_rows",
     "fg_uncook_q8_0_rows", "fg_hip_dense_q8_0_cooked", "fg_hip_output_slice_run_dense",
+    "fg_hip_output_slice_run_dense_sampled",
     "fg_sampler_hip_plan", "fg_sampler_hip_block",
     "fg_output_config_encode", "fg_output_config_decode", "fg_output_result_encode",
     "fg_output_result_decode", "fg_output_configs_batch", "fg_output_results_encode_batch",
@@ -180,6 +181,8 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_cook_q8_0_rows": (C.c_bool, [P, P, u64, u32, u32]),
         "fg_uncook_q8_0_rows": (C.c_bool, [P, P, u64, u32, u32]),
         "fg_hip_dense_q8_0_cooked": (C.c_int, [P, P, P, u32, u32, u32, f32, P, E]),
+        "fg_hip_output_slice_run_dense_sampled":
+            (C.c_int, [P, P, P, u32, u32, f32, C.POINTER(SamplerConfig), P, u64, P, P, P, P, P, E]),
         "fg_hip_output_slice_run_dense":
             (C.c_int, [P, P, P, u32, u32, f32, P, P, P, P, P, E]),
         "fg_sampler_hip_plan": (C.c_int, [u32, u32, u32, C.POINTER(Geometry), E]),
@@ -410,6 +413,23 @@ class OutputSlice:
         _check(self._lib.fg_hip_output_slice_run_dense(
             self.handle, _ptr(weights), _ptr(hidden), width, tokens, scale, _ptr(values),
             _ptr(ids), _ptr(row_status), _ptr(logits), _stream(stream), C.byref(err)), err)
+
+    def run_dense_sampled(self, weights, hidden, width, tokens, configs, uniforms, out_tokens,
+                          out_logits, row_status, counts=None, counts_stride=None, scale=1.0,
+                          stream=None):
+        """fg_hip_output_slice_run_dense_sampled: the LM head fused with
+        penalties, the top-k ladder and the select (or the greedy argmax)
+        for each token; no logits are written."""
+        if len(configs) < tokens:
+            raise ValueError(f"{len(configs)} configs for {tokens} tokens")
+        arr = (SamplerConfig * len(configs))(*configs)
+        stride = counts_stride if counts_stride is not None else (
+            counts.stride(0) if counts is not None else 0)
+        err = FgError()
+        _check(self._lib.fg_hip_output_slice_run_dense_sampled(
+            self.handle, _ptr(weights), _ptr(hidden), width, tokens, scale, arr, _ptr(counts),
+            stride, _ptr(uniforms), _ptr(out_tokens), _ptr(out_logits), _ptr(row_status),
+            _stream(stream), C.byref(err)), err)
 
     def reduce(self, logits, values, ids, row_status, batch_rows=None, stride=None, stream=None):
         batch_rows = batch_rows if batch_rows is not None else logits.shape[0]

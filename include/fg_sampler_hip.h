@@ -299,6 +299,28 @@ fg_status fg_hip_output_slice_run_dense(fg_hip_output_slice *slice, const void *
                                         int32_t *row_status, float *logits, void *stream,
                                         fg_error *err);
 
+/* fg_output_sample (src/output.c:702-756) fused with the LM head it samples
+ * from, for `tokens` hidden vectors: per token t, the logits
+ * fg_hip_dense_q8_0_cooked would write (never stored), penalties over
+ * counts[t*counts_stride + id] when fg_sampler_penalties_active(configs[t])
+ * and counts != NULL (the C rounding of fg_sampler_apply_penalties), then
+ * T == 0: the argmax (the greedy order of fg_output_better; a non-finite
+ * winner sets row_status FG_ERR_FORMAT with penalties, FG_ERR_MISMATCH
+ * without, and token 0xffffffff), or T > 0: the exact top_k (1..64) and
+ * fg_sampler_select with uniforms[t].  out_tokens[t], out_logits[t] (the
+ * penalised, untempered logit) and row_status[t] as fg_sampler_hip_sample
+ * writes them for those logits.  Whole-head slices only (ways 1, first_row
+ * 0, rows == vocab); configs are host memory, validated as
+ * fg_sampler_config_validate does (FG_ERR_ARGUMENT, "invalid sampler
+ * controls").  One launch per two tokens; calls on one slice must not
+ * overlap.  The history increment stays a separate step
+ * (fg_sampler_hip_history_increment, or the caller's own). */
+fg_status fg_hip_output_slice_run_dense_sampled(
+    fg_hip_output_slice *slice, const void *weights, const float *hidden, uint32_t in,
+    uint32_t tokens, float scale, const fg_sampler_config *configs, const uint32_t *counts,
+    uint64_t counts_stride, const float *uniforms, uint32_t *out_tokens, float *out_logits,
+    int32_t *row_status, void *stream, fg_error *err);
+
 /* The owner's combine (src/runtime.c:2440-2466) for `rows` decode rows:
  * part_*[r*ways + 0] is the owner's own finalist, part_*[r*ways + i] (i >= 1)
  * the one rank part_ranks[r*ways + i] sent.  span_first/span_rows (host
