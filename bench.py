@@ -514,6 +514,8 @@ def main():
                     help="--lm-head: the plain product writing logits (no finalist)")
     ap.add_argument("--sampled", action="store_true",
                     help="--lm-head: fused with config 2's penalties, top-k, top-p and draw")
+    ap.add_argument("--per-step-configs", action="store_true",
+                    help="upload every row's controls before every sample (the owner loop)")
     ap.add_argument("--history", action="store_true",
                     help="time the history count tables rebuilt from wire payloads")
     ap.add_argument("--topk-reduce", action="store_true",
@@ -573,9 +575,21 @@ def main():
     lpv = torch.empty((nsets if L else 1, w.rows, max(L, 1)), dtype=torch.float32, device=dev)
     lpi = torch.empty((nsets if L else 1, w.rows, max(L, 1)), dtype=torch.int32, device=dev)
 
+    # --per-step-configs: the output owner's loop, where every row's controls
+    # arrive with every token (src/protocol.c:1158-1166): fresh controls are
+    # uploaded before each sample, alternating between the workload's and a
+    # second set of the same kind (other temperatures and top-p values).
+    ctl_sets = [[c.c for c in w.configs],
+                [fg_hip.make_config(c["temperature"] * 0.9 if c["temperature"] else 0.0,
+                                    min(1.0, c["top_p"] * 0.95), c["top_k"], presence=c["presence"],
+                                    frequency=c["frequency"], repetition=c["repetition"])
+                 for c in w.configs]]
+
     def step(i):
         k = i % nsets
         x, c, u = sets[k]
+        if args.per_step_configs:
+            sampler.set_configs(ctl_sets[i % 2], flags=w.flags, stream=stream.cuda_stream)
         sampler.sample(x, u, tokens[k], counts=c, row_status=status[k], logprobs=L,
                        logprob_values=lpv[k] if L else None, logprob_ids=lpi[k] if L else None,
                        stream=stream.cuda_stream)
@@ -599,6 +613,14 @@ def main():
     written = min(nsets, args.warmup + args.steps)
     bad = int((status[:written] != 0).sum())
     assert bad == 0, f"{bad} rows of {written} written sets reported errors"
+    if args.per_step_configs:
+        # Batch 0 again with the workload's own controls, for the parity check.
+        sampler.set_configs(ctl_sets[0], flags=w.flags, stream=stream.cuda_stream)
+        x, c, u = sets[0]
+        sampler.sample(x, u, tokens[0], counts=c, row_status=status[0], logprobs=L,
+                       logprob_values=lpv[0] if L else None, logprob_ids=lpi[0] if L else None,
+                       stream=stream.cuda_stream)
+        torch.cuda.synchronize()
     x0, c0, u0 = (t.cpu().numpy() for t in sets[0])
     c0 = c0.view("uint32")
     parity = oracle_parity(
@@ -624,7 +646,9 @@ def main():
         "dtype": "f32",
         "data": f"synthetic (device-generated config-{args.config} batches, rotated over "
                 f"{nsets} distinct sets = {nsets * batch_bytes / 1e9:.2f} GB)",
-        "config": {"workload": w.name, "rows": w.rows, "vocab": VOCAB, "global_batch": w.rows,
+        "config": {"workload": w.name + (", controls uploaded every step"
+                                         if args.per_step_configs else ""),
+                   "rows": w.rows, "vocab": VOCAB, "global_batch": w.rows,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -238,20 +238,11 @@ struct Workspace {
   Tuning tuning;            // environment overrides
 };
 
-// set_configs stages each upload in its own pinned slot and records an event
-// after the copy; a slot is rewritten only after its event, so a caller that
-// changes every row's controls on every step never waits for the stream
-// unless kStageSlots uploads are still in flight.
-constexpr uint32_t kStageSlots = 8;
-
 struct fg_sampler_hip {
   int device;
   uint32_t vocab;
   Workspace ws;             // device workspace (hipMalloc'd at create)
   RowParams* h_params;      // host mirror of the uploaded table (launch-variant choice)
-  RowParams* h_stage;       // pinned [kStageSlots][max_rows]: copy sources of set_configs
-  hipEvent_t stage_done[kStageSlots];  // recorded after each slot's copy
-  uint32_t stage_next;      // slot the next set_configs fills
   uint32_t config_rows;     // rows configured by the last set_configs
   uint64_t* counters;       // event counters, FG_SAMPLE_TRACE builds only
 };
@@ -328,9 +319,9 @@ hipError_t static_workspace(Workspace* w) {
   return hipSuccess;
 }
 
-// Rows of controls per launch of static_params_kernel (2 KiB of arguments).
+// Rows of controls per launch of params_fill_kernel (2 KiB of arguments).
 constexpr uint32_t kParamsPerFill = 64;
-struct StaticParams {
+struct ParamsFill {
   RowParams rows[kParamsPerFill];
   uint32_t first;
   uint32_t count;
@@ -340,12 +331,25 @@ struct StaticParams {
 // arrival counters (a fill kernel, not a memset, so the call can sit in a
 // captured graph).
 __global__ void __launch_bounds__(kParamsPerFill)
-    static_params_kernel(StaticParams p, RowParams* params, uint32_t* row_done) {
+    params_fill_kernel(ParamsFill p, RowParams* params, uint32_t* row_done) {
   const uint32_t t = threadIdx.x;
   if (t < p.count) {
     params[p.first + t] = p.rows[t];
     row_done[static_cast<size_t>(p.first + t) * fg::kLineWords] = 0u;
   }
+}
+
+// Writes rows [0, rows) of the controls to w.params with params_fill_kernel
+// launches on `stream` (the rows travel in the kernel arguments).
+hipError_t fill_params(const Workspace& w, const RowParams* h, uint32_t rows, hipStream_t stream) {
+  for (uint32_t first = 0; first < rows; first += kParamsPerFill) {
+    ParamsFill p;
+    p.first = first;
+    p.count = rows - first < kParamsPerFill ? rows - first : kParamsPerFill;
+    memcpy(p.rows, h + first, sizeof(RowParams) * p.count);
+    params_fill_kernel<<<1, kParamsPerFill, 0, stream>>>(p, w.params, w.row_done);
+  }
+  return hipGetLastError();
 }
 
 // One fused sampling launch (two with whole-row nucleus rows) over a batch
@@ -834,11 +838,6 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMalloc(&s->ws.nuc_deep, sizeof(uint32_t) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&s->ws.nuc_max, sizeof(float) * max_rows);
   if (e == hipSuccess) e = hipMemset(s->ws.params, 0, sizeof(RowParams) * max_rows);
-  if (e == hipSuccess)
-    e = hipHostMalloc(reinterpret_cast<void**>(&s->h_stage),
-                      sizeof(RowParams) * max_rows * kStageSlots, hipHostMallocDefault);
-  for (uint32_t i = 0; i < kStageSlots && e == hipSuccess; i++)
-    e = hipEventCreateWithFlags(&s->stage_done[i], hipEventDisableTiming);
 #ifdef FG_SAMPLE_TRACE
   if (e == hipSuccess) e = hipMalloc(&s->ws.trace, sizeof(uint64_t) * 16u * (groups_cap + max_rows));
   if (e == hipSuccess) e = hipMemset(s->ws.trace, 0, sizeof(uint64_t) * 16u * (groups_cap + max_rows));
@@ -868,14 +867,6 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   (void)hipFree(s->ws.nuc_deep);
   (void)hipFree(s->ws.nuc_max);
   (void)hipFree(s->ws.trace);
-  // Pending uploads read the pinned slots: let them finish first.
-  for (uint32_t i = 0; i < kStageSlots; i++) {
-    if (s->stage_done[i]) {
-      (void)hipEventSynchronize(s->stage_done[i]);
-      (void)hipEventDestroy(s->stage_done[i]);
-    }
-  }
-  (void)hipHostFree(s->h_stage);
   free(s->h_params);
   free(s);
 }
@@ -894,19 +885,11 @@ fg_status fg_sampler_hip_set_configs(fg_sampler_hip* s, const fg_sampler_config*
   for (uint32_t r = 0; r < rows; r++) {
     s->h_params[r] = row_params(&configs[r]);
   }
-  // The copy is ordered on `stream` after earlier launches that read
-  // d_params and before later ones; only its pinned source needs guarding.
-  const uint32_t slot = s->stage_next;
-  RowParams* src = s->h_stage + static_cast<size_t>(slot) * s->ws.max_rows;
-  hipError_t e = hipEventSynchronize(s->stage_done[slot]);
-  if (e == hipSuccess) {
-    memcpy(src, s->h_params, sizeof(RowParams) * rows);
-    e = hipMemcpyAsync(s->ws.params, src, sizeof(RowParams) * rows, hipMemcpyHostToDevice,
-                       as_stream(stream));
-  }
-  if (e == hipSuccess) e = hipEventRecord(s->stage_done[slot], as_stream(stream));
+  // The controls reach the device table as arguments of fill kernels on
+  // `stream` (ordered after earlier launches that read the table and before
+  // later ones): no host copy, no staging buffer, nothing to wait for.
+  const hipError_t e = fill_params(s->ws, s->h_params, rows, as_stream(stream));
   if (e != hipSuccess) return hip_fail(err, e, "upload sampler configuration");
-  s->stage_next = (slot + 1u) % kStageSlots;
   s->config_rows = rows;
   return FG_OK;
 }
@@ -940,15 +923,8 @@ fg_status fg_sampler_hip_sample_static(uint32_t vocab, const fg_sampler_config* 
   Workspace w;
   hipError_t e = static_workspace(&w);
   if (e != hipSuccess) return hip_fail(err, e, "static sampler workspace");
-  // Controls and cleared row counters, by value through kernel arguments.
-  for (uint32_t first = 0; first < b->rows; first += kParamsPerFill) {
-    StaticParams p;
-    p.first = first;
-    p.count = b->rows - first < kParamsPerFill ? b->rows - first : kParamsPerFill;
-    memcpy(p.rows, h + first, sizeof(RowParams) * p.count);
-    static_params_kernel<<<1, kParamsPerFill, 0, as_stream(stream)>>>(p, w.params, w.row_done);
-  }
-  e = hipGetLastError();
+  // Controls by value through kernel arguments (fill kernels).
+  e = fill_params(w, h, b->rows, as_stream(stream));
   if (e != hipSuccess) return hip_fail(err, e, "static sampler controls");
   return sample_launch(w, h, vocab, b, as_stream(stream), err);
 }

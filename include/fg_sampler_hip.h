@@ -140,10 +140,10 @@ void fg_sampler_hip_destroy(fg_sampler_hip *sampler);
 
 /* Validates each row's controls as fg_sampler_config_validate does and copies
  * them to the device table used by later fg_sampler_hip_sample calls.  Row r
- * of a batch uses configs[r].  Stream-ordered and asynchronous: the table is
- * staged in one of 8 pinned host slots, copied on `stream` and guarded by an
- * event, so the call returns without waiting for the device unless 8 uploads
- * are still pending.  The reference ships these controls with every token
+ * of a batch uses configs[r].  Stream-ordered and asynchronous: the controls
+ * travel as the arguments of small fill kernels launched on `stream` (64
+ * rows each), so the call never waits for the device and needs no staging
+ * copy.  The reference ships these controls with every token
  * (src/protocol.c:1158-1166); an owner loop may call this before every
  * sample.  Launches that read the table (sample, history_increment) must be
  * on the same stream. */
