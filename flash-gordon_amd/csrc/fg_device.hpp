@@ -443,6 +443,17 @@ __device__ __forceinline__ double wave_prefix_sum_f64(double x) {
   return x + before;
 }
 
+// The same scan for u32 counts.
+__device__ __forceinline__ uint32_t wave_prefix_sum_u32(uint32_t x) {
+  x += row_shr<1>(x);
+  x += row_shr<2>(x);
+  x += row_shr<4>(x);
+  x += row_shr<8>(x);
+  const uint32_t r0 = readlane32(x, 15), r1 = readlane32(x, 31), r2 = readlane32(x, 47);
+  const uint32_t row = lane_id() >> 4;
+  return x + (row < 2u ? (row == 0u ? 0u : r0) : (row == 2u ? r0 + r1 : r0 + r1 + r2));
+}
+
 // Inclusive sum over lanes >= this lane (used by the LDS radix select).
 __device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t v) {
   const uint32_t lane = lane_id();

@@ -951,6 +951,15 @@ fg_status fg_lm_trace_copy(uint64_t* host, uint64_t count) {
 }
 #endif
 
+#ifdef FG_REDUCE_TRACE
+// Copies the top-512 reduction's phase timestamps ([tile][32]) to the host.
+fg_status fg_reduce_trace_copy(uint64_t* host, uint64_t count) {
+  const hipError_t e =
+      hipMemcpyFromSymbol(host, HIP_SYMBOL(fg::g_reduce_trace), sizeof(uint64_t) * count);
+  return e == hipSuccess ? FG_OK : FG_ERR_UNAVAILABLE;
+}
+#endif
+
 #ifdef FG_SAMPLE_TRACE
 // Copies the last launch's phase timestamps ([workgroup][8]) to the host.
 fg_status fg_sampler_hip_trace_copy(fg_sampler_hip* s, uint64_t* host, uint64_t count) {

@@ -300,56 +300,135 @@ __global__ __launch_bounds__(kWireBlock) void history_wire_count_kernel(
 // comparator (:9; padding id 0xffffffff last, non-finite first with lower id
 // first, then larger value, equal values (0 == -0) by lower id), the first
 // min(512, n) written, the rest of the 512 slots padded with (-inf,
-// 0xffffffff).  One workgroup per tile sorts (greedy composite, position)
-// pairs with a bitonic network in LDS; scores and ids are then copied from
-// the input by position, so every bit of a value (NaN payloads, -0) is kept.
+// 0xffffffff).  Entries are ordered as 64-bit greedy composites (padding ids
+// 1, the fill slots of a partial tile 0) carried with the score's bits, so
+// every bit of a value (NaN payloads, -0) is written back; the id is the
+// composite's low word.
+//
+// One 512-thread workgroup per tile; thread t holds positions t + 512 e.
+// A tile of more than 1024 entries is bucketed:
+//  1. 64 sampled composites (positions p % 64 == 37) are sorted by one wave;
+//     the region is every composite at or above the sample's 24th largest
+//     (about 37% of the tile).
+//  2. Region composites fall into 128 buckets by a monotone map of their
+//     high word (the float key) onto [region floor, tile maximum]; the
+//     buckets are counted in LDS (spread over 128 addresses, so the atomics
+//     rarely meet) and scanned from the top: the buckets down to the one
+//     holding the 512th entry are kept and scattered into LDS in bucket
+//     order.
+//  3. Each wave sorts one 64-entry window of that array (a DPP/permlane
+//     bitonic network, no barriers); a bucket that crosses a window edge is
+//     then sorted whole by one wave.  Buckets are ordered intervals, so the
+//     array is then sorted.
+// A bucket of more than 64 entries (heavily tied values) sends the tile to
+// a workgroup-wide bitonic sort of the kept entries; a region with fewer
+// than 512 entries (a sample unlike its tile) to an exact MSB-first radix
+// select.  Tiles of at most 1024 entries keep them all and take the
+// workgroup-wide sort.
 constexpr int kReduceBlock = 512;
 constexpr uint32_t kReduceTile = 4096u;
 constexpr uint32_t kReduceKeep = 512u;
+constexpr uint32_t kReduceSort = 1024u;      // most kept entries the sort takes
+constexpr uint32_t kReduceBuckets = 128u;
+constexpr uint32_t kReduceRegionRank = 23u;  // sample rank of the region floor
+constexpr uint32_t kReduceSampleLane = 37u;  // lane whose entries form the sample
+constexpr uint32_t kReduceNoBucket = 0xffu;
 
-// Per tile: a radix select (eight 8-bit digits, most significant first)
-// finds the composite of the tile's min(512, n)-th entry, the entries at or
-// above it are compacted into LDS, and only those are sorted.
-__global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
-    float* out_scores, uint32_t* out_ids, const float* in_scores, const uint32_t* in_ids,
-    uint32_t count, uint32_t out_per_tile) {
-  constexpr uint32_t kPer = kReduceTile / kReduceBlock;  // entries per thread
-  __shared__ uint32_t s_hist[256];
-  __shared__ uint32_t s_sel[3];  // chosen digit, entries above it, entries in it
-  __shared__ uint64_t s_key[kReduceKeep];
-  __shared__ uint16_t s_pos[kReduceKeep];
-  __shared__ uint32_t s_n;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t base = blockIdx.x * kReduceTile;
-  const uint32_t n = min(kReduceTile, count - base);
-  uint64_t key[kPer];
-#pragma unroll
-  for (uint32_t e = 0; e < kPer; e++) {
-    const uint32_t i = e * kReduceBlock + tid;
-    uint64_t k = 0ull;  // a fill slot of a partial tile: never selected
-    if (i < n) {
-      const uint32_t id = in_ids ? in_ids[base + i] : base + i;
-      // Padding ids rank last among the entries (1).
-      k = id == kInvalidId ? 1ull : greedy_comp(in_scores[base + i], id);
-    }
-    key[e] = k;
+#ifdef FG_REDUCE_TRACE
+// Phase timestamps of trace builds: [tile][32] (s_memrealtime, 100 MHz).
+__device__ uint64_t g_reduce_trace[512 * 32];
+#define FG_RDT(slot)                                                                    \
+  do {                                                                                  \
+    if (threadIdx.x == 0) g_reduce_trace[blockIdx.x * 32u + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define FG_RDT(slot) \
+  do {               \
+  } while (0)
+#endif
+
+struct ReduceShared {
+  uint64_t key[2][kReduceSort];  // kept entries in [0]; sort exchanges alternate
+  uint32_t bits[2][kReduceSort];  // the entries' score bits
+  uint64_t sample[kWave];        // sorted descending
+  uint64_t wave_max[kReduceBlock / kWave];
+  uint32_t hist[256];
+  uint32_t start[kReduceBuckets];
+  uint32_t straddle[kReduceBlock / kWave + 1u];
+  uint32_t sel[4];
+  uint32_t n_kept;      // radix fallback's kept entries
+  uint32_t n_straddle;  // buckets across window edges
+};
+
+// Compare-exchange of (composite, score bits) with lane ^ J: the larger key stays
+// where keep_min is false.  Composites of one tile are unique except for
+// duplicate ids, whose entries are identical, so a strict compare suffices.
+template <int J>
+__device__ __forceinline__ void cx_lanes(uint64_t& k, uint32_t& p, bool keep_min) {
+  const uint64_t ok = lane_xor64<J>(k);
+  const uint32_t op = lane_xor<J>(p);
+  const bool take = (ok > k) != keep_min;
+  k = take ? ok : k;
+  p = take ? op : p;
+}
+
+// The steps j, j/2, .., 1 (j <= 32) of the bitonic stage of block size kb for
+// element idx (descending where idx & kb == 0).
+__device__ __forceinline__ void cx_lane_steps(uint64_t& k, uint32_t& p, uint32_t idx, uint32_t kb,
+                                              uint32_t j) {
+  const bool asc = (idx & kb) != 0u;
+  switch (j) {
+    case 32u: cx_lanes<32>(k, p, asc != ((idx & 32u) != 0u)); [[fallthrough]];
+    case 16u: cx_lanes<16>(k, p, asc != ((idx & 16u) != 0u)); [[fallthrough]];
+    case 8u: cx_lanes<8>(k, p, asc != ((idx & 8u) != 0u)); [[fallthrough]];
+    case 4u: cx_lanes<4>(k, p, asc != ((idx & 4u) != 0u)); [[fallthrough]];
+    case 2u: cx_lanes<2>(k, p, asc != ((idx & 2u) != 0u)); [[fallthrough]];
+    case 1u: cx_lanes<1>(k, p, asc != ((idx & 1u) != 0u)); break;
+    default: break;
   }
-  const uint32_t want = min(kReduceKeep, n);
-  // Radix select: after digit d, `prefix` holds the top d bytes of the
-  // want-th largest key and `rank` its rank among the keys sharing them.
+}
+
+// Sorts lanes [0, w) of one wave descending (w <= 64; lanes >= w must hold
+// key 0): stages up to the first power of two >= w.
+__device__ __forceinline__ void wave_sort_pairs(uint64_t& k, uint32_t& p, uint32_t w) {
+  const uint32_t lane = lane_id();
+  for (uint32_t kb = 2u; kb <= static_cast<uint32_t>(kWave); kb <<= 1) {
+    cx_lane_steps(k, p, lane, kb, kb >> 1);
+    if (kb >= w) break;
+  }
+}
+
+// Appends this lane's entry where p holds, one LDS atomic per wave; returns
+// its slot (meaningless where p is false).
+__device__ __forceinline__ uint32_t wave_append(uint32_t* counter, bool p) {
+  const uint64_t m = ballot(p);
+  if (!m) return 0u;
+  const uint32_t lead = static_cast<uint32_t>(__builtin_ctzll(m));
+  uint32_t first = 0u;
+  if (lane_id() == lead) first = atomicAdd(counter, static_cast<uint32_t>(__builtin_popcountll(m)));
+  return readlane32(first, lead) + lanes_below(m);
+}
+
+// Exact fallback: the want-th largest of the tile's composites by an MSB-first
+// radix select, then exactly `want` entries (those above it, and as many equal
+// to it as needed) appended to the kept list.
+__device__ __forceinline__ void reduce_radix_keep(ReduceShared& S, const uint64_t (&key)[8],
+                                                  const uint32_t (&sbits)[8], uint32_t n,
+                                                  uint32_t want) {
+  constexpr uint32_t kPer = kReduceTile / kReduceBlock;
+  const uint32_t tid = threadIdx.x;
   uint64_t prefix = 0ull;
   uint32_t rank = want;
-  int last = 0;  // lowest digit selected: 4 when the top 32 bits settle it
+  uint64_t cmp_mask = ~0ull;
   for (int d = 7; d >= 0; d--) {
     const uint32_t shift = 8u * static_cast<uint32_t>(d);
     const uint64_t hi_mask = d == 7 ? 0ull : ~0ull << (shift + 8u);
-    if (tid < 256u) s_hist[tid] = 0u;
+    if (tid < 256u) S.hist[tid] = 0u;
     __syncthreads();
 #pragma unroll
     for (uint32_t e = 0; e < kPer; e++) {
       const uint32_t i = e * kReduceBlock + tid;
-      if (i < n && (key[e] & hi_mask) == prefix)
-        atomicAdd(&s_hist[(key[e] >> shift) & 255u], 1u);
+      if (i < n && (key[e] & hi_mask) == prefix) atomicAdd(&S.hist[(key[e] >> shift) & 255u], 1u);
     }
     __syncthreads();
     if (tid < 64u) {
@@ -358,43 +437,39 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
       uint32_t sum = 0u;
 #pragma unroll
       for (int b = 0; b < 4; b++) {
-        c[b] = s_hist[255u - 4u * tid - b];
+        c[b] = S.hist[255u - 4u * tid - b];
         sum += c[b];
       }
-      uint32_t before = sum;  // inclusive prefix over lanes, then made exclusive
+      uint32_t before = sum;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const uint32_t t = __shfl_up(before, o, 64);
         if (tid >= static_cast<uint32_t>(o)) before += t;
       }
-      before -= sum;
-      uint32_t acc = before;
+      uint32_t acc = before - sum;
 #pragma unroll
       for (int b = 0; b < 4; b++) {
         if (acc < rank && acc + c[b] >= rank) {
-          s_sel[0] = 255u - 4u * tid - b;
-          s_sel[1] = acc;
-          s_sel[2] = c[b];
+          S.sel[0] = 255u - 4u * tid - b;
+          S.sel[1] = acc;
+          S.sel[2] = c[b];
         }
         acc += c[b];
       }
     }
     __syncthreads();
-    prefix |= static_cast<uint64_t>(s_sel[0]) << shift;
-    rank -= s_sel[1];
-    const bool settled = d == 4 && s_sel[2] == rank;  // keep every key of this float key
+    prefix |= static_cast<uint64_t>(S.sel[0]) << shift;
+    rank -= S.sel[1];
+    const bool settled = d == 4 && S.sel[2] == rank;  // every key of this float key is kept
     __syncthreads();
     if (settled) {
-      last = 4;
+      cmp_mask = ~0ull << 32;
       break;
     }
   }
-  // Kept: keys above prefix, and `rank` keys equal to it in the digits
-  // selected (all of them when the float key settled it).
-  const uint64_t cmp_mask = last == 4 ? ~0ull << 32 : ~0ull;
   if (tid == 0) {
-    s_n = 0u;
-    s_sel[0] = 0u;
+    S.sel[3] = 0u;
+    S.n_kept = 0u;
   }
   __syncthreads();
 #pragma unroll
@@ -402,43 +477,303 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
     const uint32_t i = e * kReduceBlock + tid;
     const uint64_t km = key[e] & cmp_mask;
     bool keep = i < n && km > prefix;
-    if (i < n && km == prefix) keep = atomicAdd(&s_sel[0], 1u) < rank;
+    if (i < n && km == prefix) keep = atomicAdd(&S.sel[3], 1u) < rank;
+    const uint32_t at = wave_append(&S.n_kept, keep);
     if (keep) {
-      const uint32_t at = atomicAdd(&s_n, 1u);
-      s_key[at] = key[e];
-      s_pos[at] = static_cast<uint16_t>(i);
+      S.key[0][at] = key[e];
+      S.bits[0][at] = sbits[e];
     }
   }
-  __syncthreads();
-  // Sort the kept entries (want of them), padded to a power of two with 0.
+}
+
+// Bitonic sort of the n_sort (<= 1024) pairs in S.key[0] / S.bits[0], padded
+// with 0 to a power of two: element idx = tid (+ 512 for the second, when
+// more than 512), descending at the end; returns rank tid's pair.  Strides
+// below 64 between lanes, 64 to 256 through LDS, 512 within a thread.
+__device__ __forceinline__ void reduce_block_sort(ReduceShared& S, uint32_t n_sort, uint64_t& k0,
+                                                  uint32_t& p0) {
+  const uint32_t tid = threadIdx.x;
   uint32_t P = 1u;
-  while (P < want) P <<= 1;
-  for (uint32_t i = want + tid; i < P; i += kReduceBlock) s_key[i] = 0ull;
-  __syncthreads();
-  for (uint32_t k = 2u; k <= P; k <<= 1) {
-    for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
-      for (uint32_t q = tid; q < P / 2u; q += kReduceBlock) {
-        const uint32_t lo = 2u * j * (q / j) + (q % j);
-        const uint32_t hi = lo + j;
-        const uint64_t a = s_key[lo], b = s_key[hi];
-        const bool desc = (lo & k) == 0u;
-        if (desc ? a < b : a > b) {
-          s_key[lo] = b;
-          s_key[hi] = a;
-          const uint16_t t = s_pos[lo];
-          s_pos[lo] = s_pos[hi];
-          s_pos[hi] = t;
+  while (P < n_sort) P <<= 1;
+  k0 = tid < n_sort ? S.key[0][tid] : 0ull;
+  p0 = tid < n_sort ? S.bits[0][tid] : 0u;
+  const uint32_t i1 = tid + kReduceBlock;
+  uint64_t k1 = i1 < n_sort ? S.key[0][i1] : 0ull;
+  uint32_t p1 = i1 < n_sort ? S.bits[0][i1] : 0u;
+  uint32_t buf = 0u;
+  for (uint32_t kb = 2u; kb <= P; kb <<= 1) {
+    uint32_t j = kb >> 1;
+    // The second element lives until the last stage's 512 step has given the
+    // first one the larger of each pair.
+    const bool two = P > kReduceBlock && kb < P;
+    if (j == kReduceBlock) {
+      if (k1 > k0) {
+        const uint64_t tk = k0;
+        k0 = k1;
+        k1 = tk;
+        const uint32_t tp = p0;
+        p0 = p1;
+        p1 = tp;
+      }
+      j >>= 1;
+    }
+    for (; j >= static_cast<uint32_t>(kWave); j >>= 1) {
+      S.key[buf][tid] = k0;
+      S.bits[buf][tid] = p0;
+      if (two) {
+        S.key[buf][i1] = k1;
+        S.bits[buf][i1] = p1;
+      }
+      __syncthreads();
+      {
+        const uint64_t ok = S.key[buf][tid ^ j];
+        const uint32_t op = S.bits[buf][tid ^ j];
+        const bool take = (ok > k0) != (((tid & kb) != 0u) != ((tid & j) != 0u));
+        k0 = take ? ok : k0;
+        p0 = take ? op : p0;
+      }
+      if (two) {
+        const uint64_t ok = S.key[buf][i1 ^ j];
+        const uint32_t op = S.bits[buf][i1 ^ j];
+        const bool take = (ok > k1) != (((i1 & kb) != 0u) != ((i1 & j) != 0u));
+        k1 = take ? ok : k1;
+        p1 = take ? op : p1;
+      }
+      buf ^= 1u;
+    }
+    cx_lane_steps(k0, p0, tid, kb, j);
+    if (two) cx_lane_steps(k1, p1, i1, kb, j);
+  }
+}
+
+__global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
+    float* out_scores, uint32_t* out_ids, const float* in_scores, const uint32_t* in_ids,
+    uint32_t count, uint32_t out_per_tile) {
+  constexpr uint32_t kPer = kReduceTile / kReduceBlock;  // entries per thread
+  __shared__ ReduceShared S;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & (kWave - 1u);
+  const uint32_t wave = tid / kWave;
+  const uint32_t base = blockIdx.x * kReduceTile;
+  const uint32_t n = min(kReduceTile, count - base);
+  const uint32_t want = min(kReduceKeep, n);
+  FG_RDT(0);
+  uint64_t key[kPer];
+  uint32_t sbits[kPer], ids[kPer];
+  // Every load is issued before the first is used.
+  if (n == kReduceTile) {
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; e++) sbits[e] = __float_as_uint(in_scores[base + e * kReduceBlock + tid]);
+    if (in_ids) {
+#pragma unroll
+      for (uint32_t e = 0; e < kPer; e++) ids[e] = in_ids[base + e * kReduceBlock + tid];
+    }
+  } else {
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; e++) {
+      const uint32_t i = min(e * kReduceBlock + tid, n - 1u);
+      sbits[e] = __float_as_uint(in_scores[base + i]);
+      if (in_ids) ids[e] = in_ids[base + i];
+    }
+  }
+  uint64_t kmax = 0ull;
+#pragma unroll
+  for (uint32_t e = 0; e < kPer; e++) {
+    const uint32_t i = e * kReduceBlock + tid;
+    const uint32_t id = in_ids ? ids[e] : base + i;
+    // Padding ids rank last among the entries (1); a fill slot of a partial
+    // tile is 0 and never selected.
+    const uint64_t k = i >= n ? 0ull : (id == kInvalidId ? 1ull : greedy_comp(__uint_as_float(sbits[e]), id));
+    key[e] = k;
+    kmax = max(kmax, k);
+  }
+  FG_RDT(1);
+  uint64_t k0;
+  uint32_t p0;
+  if (n <= kReduceSort) {
+    // Every entry is kept; positions below 1024 are e = 0, 1.
+#pragma unroll
+    for (uint32_t e = 0; e < 2u; e++) {
+      const uint32_t i = e * kReduceBlock + tid;
+      if (i < n) {
+        S.key[0][i] = key[e];
+        S.bits[0][i] = sbits[e];
+      }
+    }
+    __syncthreads();
+    reduce_block_sort(S, n, k0, p0);
+  } else {
+    kmax = wave_max_u64(kmax);
+    if (lane == 0u) S.wave_max[wave] = kmax;
+    if (lane == kReduceSampleLane) {
+#pragma unroll
+      for (uint32_t e = 0; e < kPer; e++) S.key[1][wave * kPer + e] = key[e];
+    }
+    if (tid < kReduceBuckets) S.hist[tid] = 0u;
+    __syncthreads();
+    if (wave == 0u) S.sample[lane] = wave_sort_desc_u64(S.key[1][lane]);
+    __syncthreads();
+    FG_RDT(2);
+    // The bucket map: region composites (>= floor) by their high word,
+    // linearly from the floor's to the tile maximum's, onto [0, 128).
+    const uint64_t floor_key = S.sample[kReduceRegionRank];
+    uint64_t top = S.wave_max[0];
+#pragma unroll
+    for (uint32_t w = 1; w < kReduceBlock / kWave; w++) top = max(top, S.wave_max[w]);
+    const uint32_t floor_hi = static_cast<uint32_t>(floor_key >> 32);
+    const float scale = static_cast<float>(kReduceBuckets) /
+                        (static_cast<float>(static_cast<uint32_t>(top >> 32) - floor_hi) + 1.0f);
+    // The count's returned value is the entry's slot within its bucket.
+    uint8_t bucket[kPer];
+    uint32_t slot[kPer];
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; e++) {
+      const uint32_t i = e * kReduceBlock + tid;
+      uint32_t c = kReduceNoBucket;
+      slot[e] = 0u;
+      if (i < n && key[e] >= floor_key) {
+        const float f = static_cast<float>(static_cast<uint32_t>(key[e] >> 32) - floor_hi) * scale;
+        c = min(static_cast<uint32_t>(f), kReduceBuckets - 1u);
+        slot[e] = atomicAdd(&S.hist[c], 1u);
+      }
+      bucket[e] = static_cast<uint8_t>(c);
+    }
+    __syncthreads();
+    FG_RDT(3);
+    if (wave == 0u) {
+      // Lane l holds buckets 127 - 2l and 126 - 2l, the highest first.
+      const uint32_t ca = 127u - 2u * lane, cb = ca - 1u;
+      const uint32_t ha = S.hist[ca], hb = S.hist[cb];
+      const uint32_t cum = wave_prefix_sum_u32(ha + hb);
+      const uint32_t start_a = cum - ha - hb, start_b = cum - hb;
+      // The boundary bucket: the first whose inclusive count reaches want.
+      const bool hit_a = start_a < want && start_a + ha >= want;
+      const bool hit_b = start_b < want && start_b + hb >= want;
+      const uint64_t hits = ballot(hit_a || hit_b);
+      uint32_t mode = 2u, bnd = 0u, above = 0u, in_bnd = 0u;
+      if (hits) {
+        const uint32_t L = static_cast<uint32_t>(__builtin_ctzll(hits));
+        const uint32_t la = readlane32(hit_a ? 1u : 0u, L);
+        bnd = la ? 127u - 2u * L : 126u - 2u * L;
+        above = la ? readlane32(start_a, L) : readlane32(start_b, L);
+        in_bnd = la ? readlane32(ha, L) : readlane32(hb, L);
+        // Buckets at or above the boundary must each fit one wave.
+        const uint32_t big = max(ca >= bnd ? ha : 0u, cb >= bnd ? hb : 0u);
+        const uint64_t over = ballot(big > static_cast<uint32_t>(kWave));
+        mode = over ? (above + in_bnd <= kReduceSort ? 1u : 2u) : 0u;
+      }
+      S.start[ca] = start_a;
+      S.start[cb] = start_b;
+      // Buckets above the boundary that cross a 64-entry window edge: their
+      // two sorted parts are merged after the windows are sorted.
+      const bool st_a = ca > bnd && ha != 0u && (start_a / kWave) != ((start_a + ha - 1u) / kWave);
+      const bool st_b = cb > bnd && hb != 0u && (start_b / kWave) != ((start_b + hb - 1u) / kWave);
+      const uint64_t ma = ballot(st_a), mb = ballot(st_b);
+      if (st_a) S.straddle[lanes_below(ma) + lanes_below(mb)] = ca;
+      if (st_b) S.straddle[lanes_below(ma) + lanes_below(mb) + (st_a ? 1u : 0u)] = cb;
+      if (lane == 0u) {
+        S.sel[0] = mode;
+        S.sel[1] = bnd;
+        S.sel[2] = above;
+        S.sel[3] = in_bnd;
+        S.n_straddle = static_cast<uint32_t>(__builtin_popcountll(ma) + __builtin_popcountll(mb));
+      }
+    }
+    __syncthreads();
+    FG_RDT(4);
+    const uint32_t mode = S.sel[0];
+    const uint32_t bnd = S.sel[1];
+    const uint32_t above = S.sel[2];  // entries in the buckets above the boundary
+    const uint32_t in_bnd = S.sel[3];
+    if (mode != 2u) {
+      // Scatter in bucket order (every offset read before any write).
+      uint32_t at[kPer];
+#pragma unroll
+      for (uint32_t e = 0; e < kPer; e++) at[e] = S.start[bucket[e] & (kReduceBuckets - 1u)] + slot[e];
+#pragma unroll
+      for (uint32_t e = 0; e < kPer; e++) {
+        const uint32_t c = bucket[e];
+        if (c != kReduceNoBucket && c >= bnd) {
+          S.key[0][at[e]] = key[e];
+          S.bits[0][at[e]] = sbits[e];
+        }
+      }
+    } else {
+      reduce_radix_keep(S, key, sbits, n, want);
+    }
+    __syncthreads();
+    FG_RDT(5);
+    if (mode == 0u) {
+      // The entries above the boundary in windows of 64, one per wave; the
+      // boundary bucket whole on the first free wave (the last wave after
+      // the merges when all eight windows are taken).
+      const uint32_t windows = (above + kWave - 1u) / kWave;
+      if (wave < windows) {
+        const uint32_t at = wave * kWave + lane;
+        uint64_t k = at < above ? S.key[0][at] : 0ull;
+        uint32_t p = at < above ? S.bits[0][at] : 0u;
+        wave_sort_pairs(k, p, min(static_cast<uint32_t>(kWave), above - wave * kWave));
+        if (at < above) {
+          S.key[0][at] = k;
+          S.bits[0][at] = p;
+        }
+      }
+      const uint32_t bnd_wave = windows < kReduceBlock / kWave ? windows : kReduceBlock / kWave - 1u;
+      const bool bnd_first = windows < kReduceBlock / kWave;
+      if (bnd_first && wave == bnd_wave) {
+        const uint32_t at = above + lane;
+        uint64_t k = lane < in_bnd ? S.key[0][at] : 0ull;
+        uint32_t p = lane < in_bnd ? S.bits[0][at] : 0u;
+        wave_sort_pairs(k, p, in_bnd);
+        if (lane < in_bnd) {
+          S.key[0][at] = k;
+          S.bits[0][at] = p;
         }
       }
       __syncthreads();
+      FG_RDT(6);
+      const uint32_t n_strad = S.n_straddle;
+      if (wave < n_strad) {
+        // Both parts of a bucket across a window edge are sorted: the first
+        // descending in the low lanes, the second reversed in the high lanes
+        // (zeros between) form a bitonic sequence, merged in six steps.
+        const uint32_t c = S.straddle[wave];
+        const uint32_t b0 = S.start[c], h = S.hist[c];
+        const uint32_t edge = (b0 / kWave + 1u) * kWave;
+        const uint32_t l1 = edge - b0, l2 = h - l1;
+        const uint32_t src = lane < l1 ? b0 + lane : edge + (kWave - 1u - lane);
+        const bool live = lane < l1 || kWave - 1u - lane < l2;
+        uint64_t v = live ? S.key[0][src] : 0ull;
+        uint32_t q = live ? S.bits[0][src] : 0u;
+        cx_lane_steps(v, q, lane, kWave, kWave / 2u);
+        if (lane < h) {
+          S.key[0][b0 + lane] = v;
+          S.bits[0][b0 + lane] = q;
+        }
+      } else if (!bnd_first && wave == bnd_wave) {
+        const uint32_t at = above + lane;
+        uint64_t k = lane < in_bnd ? S.key[0][at] : 0ull;
+        uint32_t p = lane < in_bnd ? S.bits[0][at] : 0u;
+        wave_sort_pairs(k, p, in_bnd);
+        if (lane < in_bnd) {
+          S.key[0][at] = k;
+          S.bits[0][at] = p;
+        }
+      }
+      __syncthreads();
+      k0 = S.key[0][tid];
+      p0 = S.bits[0][tid];
+    } else {
+      reduce_block_sort(S, mode == 1u ? above + in_bnd : want, k0, p0);
     }
   }
-  for (uint32_t i = tid; i < out_per_tile; i += kReduceBlock) {
-    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * kReduceKeep + i;
-    if (i < want) {
-      const uint32_t src = base + s_pos[i];
-      out_scores[o] = in_scores[src];
-      out_ids[o] = in_ids ? in_ids[src] : src;
+  FG_RDT(7);
+
+  if (tid < out_per_tile) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * kReduceKeep + tid;
+    if (tid < want) {
+      out_scores[o] = __uint_as_float(p0);
+      out_ids[o] = k0 == 1ull ? kInvalidId : ~static_cast<uint32_t>(k0);
     } else {
       out_scores[o] = -INFINITY;
       out_ids[o] = kInvalidId;

@@ -328,6 +328,59 @@ def test_topk_reduce_matches_oracle(dev, count):
     assert np.array_equal(gi == 0xFFFFFFFF, ~real)
 
 
+def _reduce_tiles():
+    """Tiles that take each route of the per-tile selection: the entries at
+    positions p % 64 == 37 form its 64-entry sample (the kernel's layout),
+    so a tile can place the sample where it wants it."""
+    rng = np.random.default_rng(77)
+    tiles = []
+    for t in range(40):  # iid tiles: boundary buckets above and below 64 entries
+        tiles.append(rng.normal(0, 1, 4096).astype(np.float32))
+    samp = (np.arange(4096) % 64) == 37
+    t = rng.normal(0, 1, 4096).astype(np.float32)  # sample = the tile's 64 largest
+    t[samp] = np.sort(rng.normal(10, 1, 64)).astype(np.float32)
+    tiles.append(t)
+    t = rng.normal(0, 1, 4096).astype(np.float32)  # 8 huge, 56 below everything
+    v = np.full(64, -50, dtype=np.float32)
+    v[:8] = 50 + np.arange(8)
+    t[samp] = rng.permutation(v)
+    tiles.append(t)
+    tiles.append(np.full(4096, 1.5, dtype=np.float32))  # all equal: ids decide
+    tiles.append(np.sort(rng.normal(0, 1, 4096)).astype(np.float32))
+    tiles.append(np.sort(rng.normal(0, 1, 4096))[::-1].astype(np.float32).copy())
+    t = (np.round(rng.normal(0, 2, 4096)) / 2).astype(np.float32)  # few distinct values
+    t[rng.random(4096) < 0.2] = np.nan
+    tiles.append(t)
+    t = rng.normal(0, 1, 4096).astype(np.float32)  # the top half of the sample tied
+    t[samp] = np.where(np.arange(64) < 32, np.float32(3.0), t[samp])
+    tiles.append(t)
+    return np.concatenate(tiles)
+
+
+@pytest.mark.parametrize("tail", [0, 1100, 3000])
+def test_topk_reduce_selection_routes(dev, tail):
+    """Every selection route of the tile kernel (all kept, a boundary of at
+    most 64 entries, a boundary kept whole, later sample windows, the exact
+    radix fallback) against the oracle, bit-exact; a partial last tile of
+    `tail` entries; ids scattered with some padding ids."""
+    rng = np.random.default_rng(5 + tail)
+    s = _reduce_tiles()
+    if tail:
+        s = np.concatenate([s, rng.normal(0, 1, tail).astype(np.float32)])
+    count = s.size
+    ids = rng.permutation(count * 2)[:count].astype(np.uint32)
+    ids[rng.random(count) < 0.002] = 0xFFFFFFFF
+    gs, gi, produced = _reduce(dev, s, ids)
+    ws, wi = O.topk_reduce_step(s, ids)
+    assert produced == ws.size
+    real = wi != 0xFFFFFFFF
+    for g in range(produced // 512):
+        sl = slice(g * 512, (g + 1) * 512)
+        assert np.array_equal(gi[sl][real[sl]], wi[sl][real[sl]]), f"tile {g}"
+        assert np.array_equal(gs[sl][real[sl]].view(np.uint32), ws[sl][real[sl]].view(np.uint32)), f"tile {g}"
+    assert np.array_equal(gi == 0xFFFFFFFF, ~real)
+
+
 def test_topk_reduce_ladder_gives_sorted_top512(dev):
     """Iterated as the reference's QSA scan iterates it (src/qsa.c:839-851):
     the final pass holds the global top-512 in comparator order."""
