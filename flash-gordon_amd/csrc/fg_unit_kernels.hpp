@@ -307,11 +307,12 @@ __global__ __launch_bounds__(kWireBlock) void history_wire_count_kernel(
 //
 // One 512-thread workgroup per tile; thread t holds positions t + 512 e.
 // A tile of more than 1024 entries is bucketed:
-//  1. 64 sampled composites (positions p % 64 == 37) are sorted by one wave;
-//     the region is every composite at or above the sample's 24th largest
-//     (about 37% of the tile).
-//  2. Region composites fall into 128 buckets by a monotone map of their
-//     high word (the float key) onto [region floor, tile maximum]; the
+//  1. The float keys (composite high words) at 64 sampled positions
+//     (p % 64 == 37) are sorted by one wave; the region is every entry whose
+//     float key is at or above the sample's 24th largest (about 37% of the
+//     tile).
+//  2. Region entries fall into 128 buckets by a monotone map of their
+//     float key onto [region floor, tile maximum]; the
 //     buckets are counted in LDS (spread over 128 addresses, so the atomics
 //     rarely meet) and scanned from the top: the buckets down to the one
 //     holding the 512th entry are kept and scattered into LDS in bucket
@@ -350,8 +351,8 @@ __device__ uint64_t g_reduce_trace[512 * 32];
 struct ReduceShared {
   uint64_t key[2][kReduceSort];  // kept entries in [0]; sort exchanges alternate
   uint32_t bits[2][kReduceSort];  // the entries' score bits
-  uint64_t sample[kWave];        // sorted descending
-  uint64_t wave_max[kReduceBlock / kWave];
+  uint32_t sample[kWave];        // sampled float keys, then sorted descending
+  uint32_t wave_max[kReduceBlock / kWave];
   uint32_t hist[256];
   uint32_t start[kReduceBuckets];
   uint32_t straddle[kReduceBlock / kWave + 1u];
@@ -576,7 +577,7 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
       if (in_ids) ids[e] = in_ids[base + i];
     }
   }
-  uint64_t kmax = 0ull;
+  uint32_t hmax = 0u;  // largest float key (composite high word)
 #pragma unroll
   for (uint32_t e = 0; e < kPer; e++) {
     const uint32_t i = e * kReduceBlock + tid;
@@ -585,7 +586,7 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
     // tile is 0 and never selected.
     const uint64_t k = i >= n ? 0ull : (id == kInvalidId ? 1ull : greedy_comp(__uint_as_float(sbits[e]), id));
     key[e] = k;
-    kmax = max(kmax, k);
+    hmax = max(hmax, static_cast<uint32_t>(k >> 32));
   }
   FG_RDT(1);
   uint64_t k0;
@@ -603,26 +604,29 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
     __syncthreads();
     reduce_block_sort(S, n, k0, p0);
   } else {
-    kmax = wave_max_u64(kmax);
-    if (lane == 0u) S.wave_max[wave] = kmax;
+    hmax = max(hmax, lane_xor<1>(hmax));
+    hmax = max(hmax, lane_xor<2>(hmax));
+    hmax = max(hmax, lane_xor<4>(hmax));
+    hmax = max(hmax, lane_xor<8>(hmax));
+    hmax = max(hmax, lane_xor<16>(hmax));
+    hmax = max(hmax, lane_xor<32>(hmax));
+    if (lane == 0u) S.wave_max[wave] = hmax;
     if (lane == kReduceSampleLane) {
 #pragma unroll
-      for (uint32_t e = 0; e < kPer; e++) S.key[1][wave * kPer + e] = key[e];
+      for (uint32_t e = 0; e < kPer; e++) S.sample[wave * kPer + e] = static_cast<uint32_t>(key[e] >> 32);
     }
     if (tid < kReduceBuckets) S.hist[tid] = 0u;
     __syncthreads();
-    if (wave == 0u) S.sample[lane] = wave_sort_desc_u64(S.key[1][lane]);
+    if (wave == 0u) S.sample[lane] = wave_sort_desc_u32(S.sample[lane]);
     __syncthreads();
     FG_RDT(2);
-    // The bucket map: region composites (>= floor) by their high word,
-    // linearly from the floor's to the tile maximum's, onto [0, 128).
-    const uint64_t floor_key = S.sample[kReduceRegionRank];
-    uint64_t top = S.wave_max[0];
+    // The bucket map: region entries (float key >= the floor) linearly from
+    // the floor to the tile's largest float key, onto [0, 128).
+    const uint32_t floor_hi = S.sample[kReduceRegionRank];
+    uint32_t top = S.wave_max[0];
 #pragma unroll
     for (uint32_t w = 1; w < kReduceBlock / kWave; w++) top = max(top, S.wave_max[w]);
-    const uint32_t floor_hi = static_cast<uint32_t>(floor_key >> 32);
-    const float scale = static_cast<float>(kReduceBuckets) /
-                        (static_cast<float>(static_cast<uint32_t>(top >> 32) - floor_hi) + 1.0f);
+    const float scale = static_cast<float>(kReduceBuckets) / (static_cast<float>(top - floor_hi) + 1.0f);
     // The count's returned value is the entry's slot within its bucket.
     uint8_t bucket[kPer];
     uint32_t slot[kPer];
@@ -631,7 +635,7 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
       const uint32_t i = e * kReduceBlock + tid;
       uint32_t c = kReduceNoBucket;
       slot[e] = 0u;
-      if (i < n && key[e] >= floor_key) {
+      if (i < n && static_cast<uint32_t>(key[e] >> 32) >= floor_hi) {
         const float f = static_cast<float>(static_cast<uint32_t>(key[e] >> 32) - floor_hi) * scale;
         c = min(static_cast<uint32_t>(f), kReduceBuckets - 1u);
         slot[e] = atomicAdd(&S.hist[c], 1u);
