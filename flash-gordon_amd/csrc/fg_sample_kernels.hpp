@@ -78,6 +78,8 @@ struct SampleArgs {
   uint32_t split;         // chunks [0, split) run in the grid's first half, the
                           // rest in its second half (split == chunks: one layout)
   uint32_t logprobs;
+  uint32_t finisher;      // c + 1: chunk c finishes each row (tagged lists, no
+                          // counter); 0: the last arriver does
   uint32_t* tokens;
   float* token_logits;
   int32_t* row_status;
@@ -930,6 +932,15 @@ __device__ inline uint64_t spec_check(const SampleArgs& a, const RowParams& p, u
   return fin;
 }
 
+// ---- the finisher's tagged lists ----------------------------------------------
+
+// Bit 63 is free in a composite (key << 31 | id part): set on a published
+// entry, so the finisher tells a stored entry from the cleared slot (0).
+constexpr uint64_t kListTag = 1ull << 63;
+// Polls before the finisher gives up on a list (about 30 ms); the row then
+// has no candidates and reports an error rather than waiting without end.
+constexpr uint32_t kTagSpins = 1u << 20;
+
 // ---- the fused kernel ------------------------------------------------------
 
 template <class F>
@@ -1130,33 +1141,48 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
   }
   uint32_t ks0 = 0u;
+  // Finisher protocol (launches whose rows all keep top lists of at most 32
+  // over 2-8 chunks, nothing else): one chunk finishes the row, reading the
+  // other chunks' lists until every entry carries the tag; the others store
+  // their lists tagged and end, with no wait for the stores and no arrival
+  // count (measured at config 2: 0.3 us less than the last-arriver hand-off;
+  // giving chunk 0 a longer slice, so that it would usually end last, cost
+  // more stream time than the wait it saved).
+  const bool fin_mode = F::kTop && !F::kSpec && !F::kLse && !F::kNuc && a.finisher != 0u &&
+                        !greedy && kk != 0u && kk <= 32u && a.chunks <= 8u;
   if (a.chunks == 1u) {  // the whole row is in this workgroup
     if (spec) ks0 = spec_key(a, row, lane, s_ks);
-  } else {
-    // Publish the workgroup's partials with device-coherent stores.
+  } else if (fin_mode && chunk != a.finisher - 1u) {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
-    if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin);
-    if (spec && lane < static_cast<uint32_t>(kWaves))
-      store_coherent(a.spec + slot * kWaves + lane, s_ks[lane]);
-    if (lane == 0) {
-      if (F::kGreedy && greedy) store_coherent(a.greedy + slot, g);
-      if (lse) {
-        store_coherent_f64(a.lse + slot * 2, m);
-        store_coherent_f64(a.lse + slot * 2 + 1, z);
+    store_coherent(a.cand + slot * kMaxK + lane, lane < kk ? fin | kListTag : uint64_t{0});
+    return;
+  } else {
+    const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
+    if (!fin_mode) {
+      // Publish the workgroup's partials with device-coherent stores.
+      if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin);
+      if (spec && lane < static_cast<uint32_t>(kWaves))
+        store_coherent(a.spec + slot * kWaves + lane, s_ks[lane]);
+      if (lane == 0) {
+        if (F::kGreedy && greedy) store_coherent(a.greedy + slot, g);
+        if (lse) {
+          store_coherent_f64(a.lse + slot * 2, m);
+          store_coherent_f64(a.lse + slot * 2 + 1, z);
+        }
+        if (F::kNuc && nuc) {
+          store_coherent_f64(a.zsum + slot * 3, zs.m);
+          store_coherent_f64(a.zsum + slot * 3 + 1, zs.z);
+          store_coherent_f64(a.zsum + slot * 3 + 2, zs.e);
+        }
       }
-      if (F::kNuc && nuc) {
-        store_coherent_f64(a.zsum + slot * 3, zs.m);
-        store_coherent_f64(a.zsum + slot * 3 + 1, zs.z);
-        store_coherent_f64(a.zsum + slot * 3 + 2, zs.e);
-      }
+      wait_memory();  // hand-off ordering: see wait_memory()
+      FG_TRACE(a, 3);
+      uint32_t arrived = 0u;
+      if (lane == 0) arrived = atomicAdd(&a.row_done[row * kLineWords], 1u);
+      arrived = __builtin_amdgcn_readfirstlane(arrived);
+      FG_TRACE(a, 4);
+      if (arrived != a.chunks - 1u) return;
     }
-    wait_memory();  // hand-off ordering: see wait_memory()
-    FG_TRACE(a, 3);
-    uint32_t arrived = 0u;
-    if (lane == 0) arrived = atomicAdd(&a.row_done[row * kLineWords], 1u);
-    arrived = __builtin_amdgcn_readfirstlane(arrived);
-    FG_TRACE(a, 4);
-    if (arrived != a.chunks - 1u) return;
 
     // ---- last workgroup of the row: merge the other workgroups' lists ----
     const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
@@ -1172,12 +1198,53 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
         uint64_t acc = 0ull;
         for (uint32_t c0 = 0; c0 < a.chunks; c0 += 8u) {
           uint64_t x[4];
+          if (fin_mode) {
+            // The finisher (at most 8 chunks): its own list from registers
+            // (reversed in the high lanes), the others' read until every
+            // entry is tagged, then cleared.
+            const uint32_t own = a.finisher - 1u;
+            // (past kk a list is not exact: those positions count as empty)
+            const uint64_t rev = lane_reverse64(fin);
+            const uint64_t mine = (pos < kk ? (hi ? rev : fin) : 0ull) | kListTag;
+            auto fetch = [&]() {
 #pragma unroll
-          for (int t = 0; t < 4; t++) {
-            const uint32_t c = c0 + 2u * t + (hi ? 1u : 0u);
-            x[t] = (c < a.chunks && pos < kk)
-                       ? load_coherent(a.cand + (row_slot + c) * kMaxK + pos)
-                       : 0ull;
+              for (int t = 0; t < 4; t++) {
+                const uint32_t c = 2u * t + (hi ? 1u : 0u);
+                if (c != own && c < a.chunks && pos < kk)
+                  x[t] = load_coherent(a.cand + (row_slot + c) * kMaxK + pos);
+              }
+            };
+#pragma unroll
+            for (int t = 0; t < 4; t++) x[t] = 2u * t + (hi ? 1u : 0u) == own ? mine : kListTag;
+            fetch();
+            for (uint32_t spin = 0;; spin++) {
+              bool miss = false;
+#pragma unroll
+              for (int t = 0; t < 4; t++) miss |= (x[t] & kListTag) == 0ull;
+              if (ballot(miss) == 0ull) break;
+              if (spin == kTagSpins) {  // never expected: the row reports an error
+#pragma unroll
+                for (int t = 0; t < 4; t++) x[t] = kListTag;
+                break;
+              }
+              __builtin_amdgcn_s_sleep(1);
+              fetch();
+            }
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+              x[t] &= ~kListTag;
+              const uint32_t c = 2u * t + (hi ? 1u : 0u);
+              if (c != own && c < a.chunks && pos < kk)
+                store_coherent(a.cand + (row_slot + c) * kMaxK + pos, uint64_t{0});
+            }
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+              const uint32_t c = c0 + 2u * t + (hi ? 1u : 0u);
+              x[t] = (c < a.chunks && pos < kk)
+                         ? load_coherent(a.cand + (row_slot + c) * kMaxK + pos)
+                         : 0ull;
+            }
           }
           if (spec && c0 == 0u) {
             // The waves' speculative keys travel with the first lists (the
@@ -1254,7 +1321,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   if (spec) fin = spec_check(a, p, row, pen, lrow, crow, fin, kk, s_ks, ks0, s_buf[0], &s_wg_key);
   FG_TRACE(a, 6);
   finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
-  if (a.chunks != 1u && lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
+  if (a.chunks != 1u && !fin_mode && lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
   FG_TRACE(a, 7);
 }
 

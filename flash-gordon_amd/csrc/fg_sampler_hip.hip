@@ -146,6 +146,7 @@ struct Tuning {
   uint32_t front_permille = 0u;  // FG_HIP_FRONT_SHARE (500..749)
   int32_t paired = -1;           // FG_HIP_PAIRED (0 / 1)
   int32_t pace = -1;             // FG_HIP_PACE (0 / 1)
+  int32_t finisher = -1;         // FG_HIP_FINISHER (0: off, c + 1: chunk c finishes)
 };
 Tuning tuning_from_env() {
   Tuning t;
@@ -159,6 +160,7 @@ Tuning tuning_from_env() {
   }
   if (const char* v = getenv("FG_HIP_PAIRED")) t.paired = atoi(v) != 0;
   if (const char* v = getenv("FG_HIP_PACE")) t.pace = atoi(v) != 0;
+  if (const char* v = getenv("FG_HIP_FINISHER")) t.finisher = atoi(v);  // 0: off, c + 1: chunk c
   return t;
 }
 
@@ -388,6 +390,15 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
   a.wave_elems = geo.wave_elems;
   a.wave_elems_b = geo.wave_elems_b;
   a.split = geo.split;
+  {
+    // Finisher protocol (see the kernel): every row a top list of at most 32
+    // (no greedy row, no log-probs) over 2-8 chunks.
+    bool ok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= 8u && b->logprobs == 0u;
+    for (uint32_t r = 0; ok && r < b->rows; r++)
+      ok = h_params[r].temperature > 0.0f && h_params[r].top_k >= 1u && h_params[r].top_k <= 32u;
+    const uint32_t which = w.tuning.finisher > 0 ? static_cast<uint32_t>(w.tuning.finisher) - 1u : 0u;
+    a.finisher = ok && which < chunks ? which + 1u : 0u;
+  }
   a.pace = geo.pace;
   a.logprobs = b->logprobs;
   a.tokens = b->tokens;
@@ -828,6 +839,8 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   }
   if (e == hipSuccess) e = hipMalloc(&s->ws.params, sizeof(RowParams) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&s->ws.cand, sizeof(uint64_t) * slots * fg::kMaxK);
+  // The finisher protocol needs cleared lists (the finisher clears what it reads).
+  if (e == hipSuccess) e = hipMemset(s->ws.cand, 0, sizeof(uint64_t) * slots * fg::kMaxK);
   if (e == hipSuccess) e = hipMalloc(&s->ws.greedy, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.spec, sizeof(uint32_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.lse, sizeof(double) * slots * 2);

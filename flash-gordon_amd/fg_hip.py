@@ -539,4 +539,5 @@ def env_summary() -> dict:
             "target_groups": os.environ.get("FG_HIP_TARGET_GROUPS"),
             "paired": os.environ.get("FG_HIP_PAIRED"),
             "front_share": os.environ.get("FG_HIP_FRONT_SHARE"),
-            "pace": os.environ.get("FG_HIP_PACE")}
+            "pace": os.environ.get("FG_HIP_PACE"),
+            "finisher": os.environ.get("FG_HIP_FINISHER")}

@@ -132,8 +132,9 @@ typedef struct fg_sampler_hip fg_sampler_hip;
 /* Creates a sampler for rows of `vocab` logits and up to `max_rows` rows per
  * call.  Allocates the device workspace once (candidate lists, row counters);
  * the calls below allocate nothing.  Uses the current HIP device.  Reads the
- * tuning variables FG_HIP_TARGET_GROUPS, FG_HIP_PAIRED, FG_HIP_FRONT_SHARE
- * and FG_HIP_PACE (launch geometry only; results do not depend on them). */
+ * tuning variables FG_HIP_TARGET_GROUPS, FG_HIP_PAIRED, FG_HIP_FRONT_SHARE,
+ * FG_HIP_PACE and FG_HIP_FINISHER (launch geometry and hand-off only;
+ * results do not depend on them). */
 fg_status fg_sampler_hip_create(fg_sampler_hip **out, uint32_t vocab, uint32_t max_rows,
                                 fg_error *err);
 void fg_sampler_hip_destroy(fg_sampler_hip *sampler);

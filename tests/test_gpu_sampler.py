@@ -492,6 +492,40 @@ def test_paired_layout_shares(dev, monkeypatch, groups, share, k):
               f"paired nucleus groups={groups} share={share}", NUC_BOUNDARY)
 
 
+@pytest.mark.parametrize("groups,finisher,k", [(32, "1", 20), (32, "2", 32), (64, "3", 1),
+                                               (128, "1", 20), (128, "6", 32), (128, "8", 7),
+                                               (128, "0", 20)])
+def test_finisher_rows(dev, monkeypatch, groups, finisher, k):
+    """The finisher hand-off (one chunk of each row reads the others' tagged
+    lists; FG_HIP_FINISHER=c+1 picks chunk c, 0 the last-arriver hand-off):
+    16 rows over 2, 4 or 8 chunks, finishing chunks whose list sits in the
+    low or the high (reversed) lanes, top values at slice edges and in one
+    slice; three calls on one sampler with new inputs each (the finisher
+    clears the lists it reads, so a call sees none of the last one's).
+    Exact against the oracle."""
+    monkeypatch.setenv("FG_HIP_TARGET_GROUPS", str(groups))
+    monkeypatch.setenv("FG_HIP_FINISHER", finisher)
+    rows, vocab = 16, W.V
+    s = fg_hip.HipSampler(vocab, rows)
+    for call in range(3):
+        rng = np.random.default_rng(groups * 10 + int(finisher) + 100 * call + k)
+        logits = rng.normal(0, 1, (rows, vocab)).astype(np.float32)
+        logits[0, :600] = 50 + rng.normal(0, 1, 600)
+        logits[1] = np.linspace(-5, 5, vocab, dtype=np.float32)
+        logits[2, 75_000:80_000] = 20 + rng.normal(0, 1, 5000)
+        logits[3, 151_000:] = 40 + rng.normal(0, 1, vocab - 151_000)
+        logits[4, :] = 1.0
+        logits[4, 98_000:98_100] = 2.0
+        counts = np.zeros((rows, vocab), dtype=np.uint32)
+        counts[7, :300] = rng.integers(1, 5, 300)
+        logits[7, :300] = 60.0
+        configs = [W.cfg(0.8, 0.9, k, presence=0.4 if r == 7 else 0.0) for r in range(rows)]
+        w = dict(logits=logits, counts=counts, configs=configs,
+                 uniforms=rng.random(rows).astype(np.float32), logprobs=0)
+        check(w, run_hip(w, dev, sampler=s), W.oracle_run(w),
+              f"finisher groups={groups} finisher={finisher} k={k} call={call}")
+
+
 @pytest.mark.parametrize("nucleus", [False, True])
 def test_graph_replays_match_eager(dev, nucleus):
     """One sample call captured in a HIP graph (the launch allocates and
