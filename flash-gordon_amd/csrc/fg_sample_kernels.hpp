@@ -1155,6 +1155,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   } else if (fin_mode && chunk != a.finisher - 1u) {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
     store_coherent(a.cand + slot * kMaxK + lane, lane < kk ? fin | kListTag : uint64_t{0});
+    FG_TRACE(a, 3);
     return;
   } else {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
