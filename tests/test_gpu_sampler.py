@@ -526,6 +526,23 @@ def test_finisher_rows(dev, monkeypatch, groups, finisher, k):
               f"finisher groups={groups} finisher={finisher} k={k} call={call}")
 
 
+def test_finisher_and_last_arriver_calls_alternate(dev):
+    """One sampler, calls that alternate between the finisher hand-off (top-k
+    rows only) and the last-arriver one (a greedy row, or log-probs, in the
+    batch): each call leaves the workspace as the next one needs it (lists
+    cleared, row counters at zero).  Exact against the oracle."""
+    rows = 16
+    s = fg_hip.HipSampler(W.V, rows)
+    for call in range(6):
+        w = W.config2(rows=rows)
+        w["logits"] = np.roll(w["logits"], 7919 * call, axis=1)  # new data each call
+        if call % 3 == 1:
+            w["configs"][5] = W.cfg(0.0, 1.0, 1)  # a greedy row
+        if call % 3 == 2:
+            w["logprobs"] = 5
+        check(w, run_hip(w, dev, sampler=s), W.oracle_run(w), f"alternating call {call}")
+
+
 @pytest.mark.parametrize("nucleus", [False, True])
 def test_graph_replays_match_eager(dev, nucleus):
     """One sample call captured in a HIP graph (the launch allocates and
