@@ -361,7 +361,7 @@ def history_bench(args, torch, fg_hip, dev):
                    "history": hist, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(alg / per_s / 1e9, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(alg / per_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "fg::history_wire_clear_kernel",
+                     "traffic": None, "kernel": "fg::history_wire_build_kernel",
                      "algorithmic_bytes_per_launch": alg, "launch_us": round(per_s * 1e6, 3)},
         "wall_s": round(wall, 3)}))
 

@@ -764,12 +764,11 @@ fg_status fg_hip_history_build_wire(uint32_t* counts, uint64_t counts_stride, ui
       counts_stride < vocab)
     return arg_fail(err, "invalid output history payloads");
   hipStream_t s = as_stream(stream);
-  if (static_cast<uint64_t>(rows) * fg::kWireChunks > 0x7fffffffu)
+  const uint32_t chunks = (vocab + fg::kWireRegion - 1u) / fg::kWireRegion;
+  if (static_cast<uint64_t>(rows) * chunks > 0x7fffffffu)
     return arg_fail(err, "invalid output history payloads");
-  fg::history_wire_clear_kernel<<<rows * fg::kWireChunks, fg::kWireBlock, 0, s>>>(
-      counts, counts_stride, vocab, payloads, offsets, row_status, row_slot);
-  fg::history_wire_count_kernel<<<rows * fg::kWireCountGroups, fg::kWireBlock, 0, s>>>(
-      counts, counts_stride, payloads, offsets, row_status);
+  fg::history_wire_build_kernel<<<rows * chunks, fg::kWireBlock, 0, s>>>(
+      counts, counts_stride, vocab, payloads, offsets, row_status, row_slot, chunks);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "history wire launch");
 }

@@ -199,15 +199,17 @@ __global__ __launch_bounds__(256) void history_increment_kernel(uint32_t* counts
 }
 
 // FG_MSG_OUTPUT_HISTORY payloads (src/protocol.c:1348-1366) decoded on the
-// device and turned into count tables (src/output.c:601-617), in two
-// launches: kWireChunks workgroups per row each validate the whole payload
-// and clear their part of the row (the first one writes the row's status),
-// then a counting launch adds the row's ids.  A row that fails validation
-// keeps its counts; its status says why (FG_ERR_ARGUMENT: shorter than the
-// header; FG_ERR_FORMAT: the decoder's other checks).  Payload bytes are
-// big-endian and need not be aligned.
+// device and turned into count tables (src/output.c:601-617) in one launch:
+// each workgroup owns kWireRegion counts of one row, validates the row's
+// whole payload (a few KB, shared through the cache by the row's
+// workgroups), counts the ids that fall in its region in LDS, and writes the
+// region once (cleared and counted in one store per entry: no clearing pass
+// and no global atomics).  The first workgroup of a row writes its status.  A
+// row that fails validation keeps its counts; its status says why
+// (FG_ERR_ARGUMENT: shorter than the header; FG_ERR_FORMAT: the decoder's
+// other checks).  Payload bytes are big-endian and need not be aligned.
 constexpr int kWireBlock = 256;
-constexpr uint32_t kWireChunks = 16u;  // clearing workgroups per row
+constexpr uint32_t kWireRegion = 8192u;  // counts per workgroup (32 KB of LDS)
 constexpr uint32_t kWireHeader = 8u;
 constexpr uint32_t kWireMaxCount = 262144u;
 constexpr uint32_t kWireMaxSlots = 2u;
@@ -217,82 +219,80 @@ __device__ __forceinline__ uint32_t load_be32(const uint8_t* p) {
          (static_cast<uint32_t>(p[2]) << 8) | static_cast<uint32_t>(p[3]);
 }
 
-// Status of row r's payload (0, 2 or 4) and its id count; every thread of
-// the workgroup returns the same.
-__device__ inline int32_t wire_validate(const uint8_t* p, uint64_t bytes, uint32_t vocab,
-                                        uint32_t* count_out, uint8_t* slot_out) {
+// Id i of a payload (big-endian, at byte 8 + 4i): one dword load when the
+// payload is 4-byte aligned, bytes otherwise.
+__device__ __forceinline__ uint32_t wire_id(const uint8_t* p, bool aligned, uint32_t i) {
+  if (aligned) return __builtin_bswap32(reinterpret_cast<const uint32_t*>(p + kWireHeader)[i]);
+  return load_be32(p + kWireHeader + 4u * i);
+}
+
+// Grid chunks * rows (chunks = ceil(vocab / kWireRegion)): workgroup b owns
+// region b % chunks of row b / chunks.  The ids are read once, right away
+// (their number follows from the payload's size): each is checked against
+// the vocabulary and, when it falls in the region, counted in LDS; the
+// header is checked alongside.  The row's region is written only when the
+// whole payload is valid.
+__global__ __launch_bounds__(kWireBlock) void history_wire_build_kernel(
+    uint32_t* counts, uint64_t stride, uint32_t vocab, const uint8_t* payloads,
+    const uint64_t* offsets, int32_t* row_status, uint8_t* row_slot, uint32_t chunks) {
+  __shared__ __align__(16) uint32_t s_cnt[kWireRegion];
   __shared__ int32_t s_status;
-  __shared__ uint32_t s_count;
-  __shared__ uint8_t s_slot;
-  if (threadIdx.x == 0) {
-    int32_t st = 0;
-    uint32_t count = 0u;
-    uint8_t slot = 0u;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t r = blockIdx.x / chunks;
+  const uint32_t chunk = blockIdx.x - r * chunks;
+  const uint8_t* p = payloads + offsets[r];
+  const uint64_t bytes = offsets[r + 1] - offsets[r];
+  const bool aligned = (reinterpret_cast<uintptr_t>(p) & 3u) == 0u;
+  // As many ids as the size allows (the header must agree, checked below).
+  const uint32_t n = bytes >= kWireHeader + 4ull * kWireMaxCount
+                         ? kWireMaxCount
+                         : (bytes >= kWireHeader ? static_cast<uint32_t>((bytes - kWireHeader) / 4u) : 0u);
+  const uint32_t begin = chunk * kWireRegion;
+  const uint32_t end = vocab - begin < kWireRegion ? vocab : begin + kWireRegion;
+  for (uint32_t i = tid; i < kWireRegion / 4u; i += kWireBlock)
+    reinterpret_cast<u4*>(s_cnt)[i] = u4{0u, 0u, 0u, 0u};
+  if (tid == 0) s_status = 0;
+  __syncthreads();
+  int32_t bad = 0;
+  for (uint32_t i = tid; i < n; i += kWireBlock) {
+    const uint32_t id = wire_id(p, aligned, i);
+    bad |= id >= vocab ? 4 : 0;
+    if (id >= begin && id < end) atomicAdd(&s_cnt[id - begin], 1u);
+  }
+  uint8_t slot = 0u;
+  if (tid == 0) {
     if (bytes < kWireHeader) {
-      st = 2;  // FG_ERR_ARGUMENT
+      bad = 2;  // FG_ERR_ARGUMENT (a short payload has no ids)
     } else {
-      count = load_be32(p);
+      const uint32_t count = load_be32(p);
       const uint32_t reserved = (static_cast<uint32_t>(p[5]) << 16) |
                                 (static_cast<uint32_t>(p[6]) << 8) | p[7];
-      if (reserved || p[4] >= kWireMaxSlots || count > kWireMaxCount ||
-          kWireHeader + 4ull * count != bytes)
-        st = 4;  // FG_ERR_FORMAT
       slot = p[4];
+      if (reserved || slot >= kWireMaxSlots || count > kWireMaxCount ||
+          kWireHeader + 4ull * count != bytes)
+        bad |= 4;  // FG_ERR_FORMAT
     }
-    s_status = st;
-    s_count = st == 0 ? count : 0u;
-    s_slot = st == 0 ? slot : 0u;
   }
+  if (bad) atomicOr(&s_status, bad);
   __syncthreads();
-  const uint32_t count = s_count;
-  for (uint32_t i = threadIdx.x; i < count; i += kWireBlock)
-    if (load_be32(p + kWireHeader + 4u * i) >= vocab) atomicOr(&s_status, 4);
-  __syncthreads();
-  *count_out = count;
-  *slot_out = s_slot;
-  return s_status;
-}
-
-// Grid kWireChunks * rows: workgroup b clears chunk b % kWireChunks of row
-// b / kWireChunks.
-__global__ __launch_bounds__(kWireBlock) void history_wire_clear_kernel(
-    uint32_t* counts, uint64_t stride, uint32_t vocab, const uint8_t* payloads,
-    const uint64_t* offsets, int32_t* row_status, uint8_t* row_slot) {
-  const uint32_t r = blockIdx.x / kWireChunks;
-  const uint32_t chunk = blockIdx.x - r * kWireChunks;
-  const uint8_t* p = payloads + offsets[r];
-  uint32_t count;
-  uint8_t slot;
-  const int32_t st = wire_validate(p, offsets[r + 1] - offsets[r], vocab, &count, &slot);
-  if (chunk == 0 && threadIdx.x == 0) {
+  // FG_ERR_ARGUMENT over FG_ERR_FORMAT, as the decoder checks the length
+  // first.
+  const int32_t st = (s_status & 2) ? 2 : s_status;
+  if (chunk == 0 && tid == 0) {
     row_status[r] = st;
-    if (row_slot && st != 2) row_slot[r] = slot;
+    if (row_slot && st != 2) row_slot[r] = st == 0 ? slot : 0u;
   }
   if (st != 0) return;
-  const uint32_t per = (vocab + kWireChunks - 1u) / kWireChunks;
-  const uint32_t begin = chunk * per;
-  const uint32_t end = begin + per < vocab ? begin + per : vocab;
   uint32_t* crow = counts + static_cast<uint64_t>(r) * stride;
-  for (uint32_t i = begin + threadIdx.x; i < end; i += kWireBlock) crow[i] = 0u;
-}
-
-// Grid kWireCountGroups * rows: the ids of each valid row, once the clearing
-// launch is done.
-constexpr uint32_t kWireCountGroups = 8u;
-__global__ __launch_bounds__(kWireBlock) void history_wire_count_kernel(
-    uint32_t* counts, uint64_t stride, const uint8_t* payloads, const uint64_t* offsets,
-    const int32_t* row_status) {
-  const uint32_t r = blockIdx.x / kWireCountGroups;
-  const uint32_t g = blockIdx.x - r * kWireCountGroups;
-  if (row_status[r] != 0) return;
-  const uint8_t* p = payloads + offsets[r];
-  const uint32_t count = load_be32(p);
-  uint32_t* crow = counts + static_cast<uint64_t>(r) * stride;
-  // The row was cleared and holds at most kWireMaxCount ids, so no count can
-  // reach UINT32_MAX: a plain atomic add saturates nothing and keeps hot ids
-  // (a Zipf history repeats its head tokens) free of compare-and-swap retries.
-  for (uint32_t i = g * kWireBlock + threadIdx.x; i < count; i += kWireCountGroups * kWireBlock)
-    atomicAdd(crow + load_be32(p + kWireHeader + 4u * i), 1u);
+  if ((reinterpret_cast<uintptr_t>(crow + begin) & 15u) == 0u) {
+    // 16-byte stores over the region's whole quads, then the tail.
+    const uint32_t quads = (end - begin) / 4u;
+    for (uint32_t q = tid; q < quads; q += kWireBlock)
+      reinterpret_cast<u4*>(crow + begin)[q] = reinterpret_cast<const u4*>(s_cnt)[q];
+    for (uint32_t i = begin + 4u * quads + tid; i < end; i += kWireBlock) crow[i] = s_cnt[i - begin];
+  } else {
+    for (uint32_t i = begin + tid; i < end; i += kWireBlock) crow[i] = s_cnt[i - begin];
+  }
 }
 
 // Top-512 reduction of shaders/fg_topk_reduce_v2.comp (src/vk.c:2235): per

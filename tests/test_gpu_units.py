@@ -192,12 +192,16 @@ def test_history_build_matches_oracle(dev):
     assert e.value.code == fg_hip.FG_ERR_FORMAT
 
 
-def test_history_build_wire_matches_oracle(dev):
+@pytest.mark.parametrize("pad,extra", [(1, 5), (0, 8)])
+def test_history_build_wire_matches_oracle(dev, pad, extra):
     """fg_hip_history_build_wire: valid payloads (Zipf histories with repeats,
-    empty, one token, slot 1, an unaligned start) rebuild their rows; every
-    malformation the decoder checks leaves its row's counts untouched and
-    reports the decoder's status (oracle: the restated decoder, pinned to the
-    reference's compiled codec)."""
+    empty, one token, slot 1, aligned and unaligned starts) rebuild their
+    rows; every malformation the decoder checks leaves its row's counts
+    untouched and reports the decoder's status (oracle: the restated decoder,
+    pinned to the reference's compiled codec).  pad shifts the blob (byte
+    loads of the ids when odd, dword loads when payloads are 4-byte
+    aligned); extra pads the row stride (16-byte stores of the counts when
+    rows stay aligned)."""
     import struct
     import torch
     vocab = 151_936
@@ -219,7 +223,7 @@ def test_history_build_wire_matches_oracle(dev):
         b"\0\0\0",                                  # shorter than the header
         wire(ids[2].tolist()),                      # valid
     ]
-    blob = bytearray(b"\x5a")                       # one pad byte: payload 0 starts unaligned
+    blob = bytearray(b"\x5a" * pad)                 # a pad byte: payload 0 starts unaligned
     offsets = []
     for pl in payloads:
         offsets.append(len(blob))
@@ -228,7 +232,7 @@ def test_history_build_wire_matches_oracle(dev):
     rows = len(payloads)
     d_blob = torch.from_numpy(np.frombuffer(bytes(blob), dtype=np.uint8).copy()).to(dev)
     d_off = torch.tensor(offsets, dtype=torch.int64, device=dev)
-    stride = vocab + 5
+    stride = vocab + extra
     counts = torch.full((rows, stride), 77, dtype=torch.int32, device=dev)
     status = torch.full((rows,), -1, dtype=torch.int32, device=dev)
     slots = torch.full((rows,), 9, dtype=torch.uint8, device=dev)
