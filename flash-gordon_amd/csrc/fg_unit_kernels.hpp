@@ -317,10 +317,11 @@ __global__ __launch_bounds__(kWireBlock) void history_wire_build_kernel(
 //     rarely meet) and scanned from the top: the buckets down to the one
 //     holding the 512th entry are kept and scattered into LDS in bucket
 //     order.
-//  3. Each wave sorts one 64-entry window of that array (a DPP/permlane
-//     bitonic network, no barriers); a bucket that crosses a window edge is
-//     then sorted whole by one wave.  Buckets are ordered intervals, so the
-//     array is then sorted.
+//  3. Each wave sorts one 64-entry window of the entries above the boundary
+//     bucket (a DPP/permlane bitonic network, no barriers), and a spare wave
+//     sorts the boundary bucket; then a bucket that crosses a window edge
+//     has its two sorted parts merged by one wave.  Buckets are ordered
+//     intervals, so the array is then sorted.
 // A bucket of more than 64 entries (heavily tied values) sends the tile to
 // a workgroup-wide bitonic sort of the kept entries; a region with fewer
 // than 512 entries (a sample unlike its tile) to an exact MSB-first radix
@@ -340,7 +341,8 @@ constexpr uint32_t kReduceNoBucket = 0xffu;
 __device__ uint64_t g_reduce_trace[512 * 32];
 #define FG_RDT(slot)                                                                    \
   do {                                                                                  \
-    if (threadIdx.x == 0) g_reduce_trace[blockIdx.x * 32u + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+    if (threadIdx.x == 0 && blockIdx.x < 512u)                                        \
+      g_reduce_trace[blockIdx.x * 32u + (slot)] = __builtin_amdgcn_s_memrealtime();     \
   } while (0)
 #else
 #define FG_RDT(slot) \
