@@ -57,16 +57,43 @@ __global__ __launch_bounds__(kSliceBlock) void slice_finalist_kernel(
       q[l] = i < slice_rows ? *reinterpret_cast<const float4*>(x + i)
                             : make_float4(-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX);
     }
+    // Past the slice end the lanes hold -FLT_MAX, the smallest finite key:
+    // it never beats an earlier real entry of the thread, and a thread whose
+    // best is such a lane has best_pos past the end (masked below).
+    // While every value is finite the float order is the key order (-0 and
+    // +0 compare equal, as their keys do), so the scan keeps the first
+    // largest value and its slot l * 4 + component (four instructions per
+    // logit); v * 0 accumulates to NaN once a value is non-finite, and only
+    // then are the keys built.
+    float bv = -INFINITY, bad = 0.0f;
+    uint32_t slot = 0u;
+    auto scan = [&](float v, uint32_t s) {
+      bad = __builtin_fmaf(v, 0.0f, bad);
+      const bool take = v > bv;
+      bv = take ? v : bv;
+      slot = take ? s : slot;
+    };
 #pragma unroll
     for (uint32_t l = 0; l < kLoads; l++) {
-      // Past the slice end the lanes hold -FLT_MAX, the smallest finite key:
-      // it never beats an earlier real entry of the thread, and a thread
-      // whose best is such a lane has best_pos past the end (masked below).
-      const uint32_t i = base + 4u * (l * kSliceBlock + threadIdx.x);
-      visit(q[l].x, i);
-      visit(q[l].y, i + 1u);
-      visit(q[l].z, i + 2u);
-      visit(q[l].w, i + 3u);
+      scan(q[l].x, 4u * l);
+      scan(q[l].y, 4u * l + 1u);
+      scan(q[l].z, 4u * l + 2u);
+      scan(q[l].w, 4u * l + 3u);
+    }
+    if (bad == 0.0f) {
+      uint32_t b = __float_as_uint(bv);
+      b = b == 0x80000000u ? 0u : b;
+      best_key = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+      best_pos = base + 4u * ((slot >> 2) * kSliceBlock + threadIdx.x) + (slot & 3u);
+    } else {
+#pragma unroll
+      for (uint32_t l = 0; l < kLoads; l++) {
+        const uint32_t i = base + 4u * (l * kSliceBlock + threadIdx.x);
+        visit(q[l].x, i);
+        visit(q[l].y, i + 1u);
+        visit(q[l].z, i + 2u);
+        visit(q[l].w, i + 3u);
+      }
     }
   } else {
     const uint32_t end = min(base + kSliceChunk, slice_rows);
