@@ -101,18 +101,38 @@ struct SampleArgs {
 
 // Phase timestamps (s_memrealtime, 100 MHz) for builds with FG_SAMPLE_TRACE;
 // compiled out otherwise.
+// The stamps go to LDS and are copied out where the workgroup's work ends
+// (FG_TRACE_FLUSH): a global store per stamp would make the compiler wait for
+// its completion before reusing the stamp's registers.
 #ifdef FG_SAMPLE_TRACE
-#define FG_TRACE(a, slot)                                                          \
-  do {                                                                             \
-    if (threadIdx.x == 0 && (a).trace)                                             \
-      (a).trace[static_cast<uint64_t>(blockIdx.x) * 16u + (slot)] =                \
-          __builtin_amdgcn_s_memrealtime();                                        \
+#define FG_TRACE_DECL __shared__ uint64_t s_trace[16]
+#define FG_TRACE_INIT                                     \
+  do {                                                    \
+    if (threadIdx.x == 0)                                 \
+      for (int i_ = 0; i_ < 16; i_++) s_trace[i_] = 0ull; \
+  } while (0)
+#define FG_TRACE(a, slot)                                              \
+  do {                                                                 \
+    if (threadIdx.x == 0) s_trace[slot] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define FG_TRACE_FLUSH(a)                                                      \
+  do {                                                                         \
+    if (threadIdx.x == 0 && (a).trace)                                         \
+      for (int i_ = 0; i_ < 16; i_++)                                          \
+        (a).trace[static_cast<uint64_t>(blockIdx.x) * 16u + i_] = s_trace[i_]; \
   } while (0)
 // Event counters of FG_SAMPLE_TRACE builds (FG_SAMPLE_COUNT also set; they
 // slow the launch down): g_trace_counters[i].
 __device__ uint64_t* g_trace_counters;
 #else
+#define FG_TRACE_DECL static_assert(true, "")
+#define FG_TRACE_INIT \
+  do {                \
+  } while (0)
 #define FG_TRACE(a, slot) \
+  do {                    \
+  } while (0)
+#define FG_TRACE_FLUSH(a) \
   do {                    \
   } while (0)
 #endif
@@ -941,6 +961,52 @@ constexpr uint64_t kListTag = 1ull << 63;
 // has no candidates and reports an error rather than waiting without end.
 constexpr uint32_t kTagSpins = 1u << 20;
 
+// ---- merging by rank ----------------------------------------------------------
+//
+// Lists of at most 32 entries are merged in LDS: every entry finds its rank
+// in the union as the sum, over the lists, of the entries above it (a
+// five-step binary search per list; the lists' searches are independent, so
+// they overlap), and the entries ranked below kk are stored at their ranks.
+// That is a few LDS round trips deep, where a bitonic merge tree runs six
+// dependent exchange steps per level.  Entries are distinct within a row.
+
+// Stores e (an entry of one of the kN descending lists at lists + i * stride,
+// positions 0..31, zeros past their ends; or 0 for none) at out[rank] when
+// its rank in their union is below kk.  The searches advance a step at a
+// time over all lists, so each step's reads are issued together.
+template <int kN>
+__device__ __forceinline__ void rank_place(const uint64_t* lists, uint32_t stride, uint64_t e,
+                                           uint32_t kk, uint64_t* out) {
+  uint32_t lo[kN];
+#pragma unroll
+  for (int i = 0; i < kN; i++) lo[i] = lists[i * stride + 15u] > e ? 16u : 0u;
+#pragma unroll
+  for (uint32_t h = 8u; h >= 1u; h /= 2u) {
+#pragma unroll
+    for (int i = 0; i < kN; i++) lo[i] += lists[i * stride + lo[i] + h - 1u] > e ? h : 0u;
+  }
+  // The search tells 31 entries above e from 32 only with the last entry,
+  // which is empty unless the lists hold 32.
+  if (kk == 32u) {
+#pragma unroll
+    for (int i = 0; i < kN; i++) lo[i] += (lo[i] == 31u && lists[i * stride + 31u] > e) ? 1u : 0u;
+  }
+  uint32_t r = 0u;
+#pragma unroll
+  for (int i = 0; i < kN; i++) r += lo[i];
+  if (e != 0ull && r < kk) out[r] = e;
+}
+
+// The finisher's eight lists in LDS (list c at lists + 32 c): lanes 0-31 of
+// wave w place the entries of list 2w, lanes 32-63 those of list 2w + 1.
+__device__ __forceinline__ void rank_place_lists(const uint64_t* lists, uint32_t wave,
+                                                 uint32_t kk, uint64_t* out) {
+  const uint32_t lane = lane_id();
+  const uint32_t c = 2u * wave + (lane >= 32u ? 1u : 0u);
+  const uint32_t pos = lane & 31u;
+  rank_place<8>(lists, 32u, pos < kk ? lists[c * 32u + pos] : 0ull, kk, out);
+}
+
 // ---- the fused kernel ------------------------------------------------------
 
 template <class F>
@@ -955,6 +1021,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   __shared__ double s_nz[kWaves];
   __shared__ double s_ne[kWaves];
   __shared__ uint32_t s_wg_key;
+  __shared__ uint64_t s_rank[32];
+  FG_TRACE_DECL;
+  FG_TRACE_INIT;
 
   // readfirstlane: the wave index is uniform across the wave, so the slice
   // bounds, buffer descriptors and loop control stay scalar (the compiler
@@ -1100,7 +1169,21 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   if (F::kNuc && nuc) wmass = wave_mass_combine(static_cast<double>(st.nm), st.nz, st.ne);
 
   // ---- the workgroup's result: wave 0 combines the four waves from LDS ----
+  // Finisher protocol (launches whose rows all keep top lists of at most 32
+  // over 2-8 chunks, nothing else): one chunk finishes the row, reading the
+  // other chunks' lists until every entry carries the tag; the others store
+  // their lists tagged and end, with no wait for the stores and no arrival
+  // count (measured at config 2: 0.3 us less than the last-arriver hand-off;
+  // giving chunk 0 a longer slice, so that it would usually end last, cost
+  // more stream time than the wait it saved).  All four waves of the
+  // finishing workgroup rank the lists.
+  const bool fin_mode = F::kTop && !F::kSpec && !F::kLse && !F::kNuc && a.finisher != 0u &&
+                        !greedy && kk != 0u && kk <= 32u && a.chunks <= 8u;
+  const bool fin_wg = fin_mode && a.chunks != 1u && chunk == a.finisher - 1u;
+  // Lists of at most 32: the four waves rank their own entries.
+  const bool rank_wg = F::kTop && kk != 0u && kk <= 32u;
   if (F::kTop) s_top[wave][lane] = mine;
+  if (F::kTop && rank_wg && wave == 0 && lane < 32u) s_rank[lane] = 0ull;
   if (lane == 0) {
     s_greedy[wave] = gbest;
     if (F::kSpec) s_ks[wave] = st.KS;
@@ -1111,23 +1194,26 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     s_ne[wave] = wmass.e;
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (F::kTop && rank_wg) {
+    rank_place<kWaves>(&s_top[0][0], kWave, mine, kk, s_rank);
+    __syncthreads();
+  }
+  if (wave != 0) {
+    if (F::kTop && fin_wg) {
+      // The finisher's helpers: wave 0 fills the lists, all four rank them.
+      __syncthreads();
+      rank_place_lists(&s_top[0][0], wave, kk, s_rank);
+      __syncthreads();
+    }
+    return;
+  }
   uint64_t fin = 0ull;
   uint64_t g = 0ull;
   double m = -INFINITY, z = 0.0;
   Mass zs{-INFINITY, 0.0, 0.0};
   if (F::kTop && kk) {
     if (kk <= 32u) {
-      // Two lists per register, the second read in reverse into lanes
-      // 32-63 (a bitonic pair), then the two results the same way.
-      const bool hi = lane >= 32u;
-      const uint32_t pos = hi ? 63u - lane : lane;
-      uint64_t a0 = hi ? s_top[1][pos] : s_top[0][pos];
-      uint64_t a1 = hi ? s_top[3][pos] : s_top[2][pos];
-      a0 = bitonic_merge_stage<64>(a0);
-      a1 = bitonic_merge_stage<64>(a1);
-      const uint64_t r1 = lane_reverse64(a1);
-      fin = bitonic_merge_stage<64>(hi ? r1 : a0);
+      fin = lane < 32u ? s_rank[lane] : 0ull;
     } else {
       // (0,1) and (2,3) side by side, then the two results.
       uint64_t a0 = s_top[0][lane], a1 = s_top[2][lane];
@@ -1141,21 +1227,13 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
   }
   uint32_t ks0 = 0u;
-  // Finisher protocol (launches whose rows all keep top lists of at most 32
-  // over 2-8 chunks, nothing else): one chunk finishes the row, reading the
-  // other chunks' lists until every entry carries the tag; the others store
-  // their lists tagged and end, with no wait for the stores and no arrival
-  // count (measured at config 2: 0.3 us less than the last-arriver hand-off;
-  // giving chunk 0 a longer slice, so that it would usually end last, cost
-  // more stream time than the wait it saved).
-  const bool fin_mode = F::kTop && !F::kSpec && !F::kLse && !F::kNuc && a.finisher != 0u &&
-                        !greedy && kk != 0u && kk <= 32u && a.chunks <= 8u;
   if (a.chunks == 1u) {  // the whole row is in this workgroup
     if (spec) ks0 = spec_key(a, row, lane, s_ks);
   } else if (fin_mode && chunk != a.finisher - 1u) {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
     store_coherent(a.cand + slot * kMaxK + lane, lane < kk ? fin | kListTag : uint64_t{0});
     FG_TRACE(a, 3);
+    FG_TRACE_FLUSH(a);
     return;
   } else {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
@@ -1182,12 +1260,66 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       if (lane == 0) arrived = atomicAdd(&a.row_done[row * kLineWords], 1u);
       arrived = __builtin_amdgcn_readfirstlane(arrived);
       FG_TRACE(a, 4);
-      if (arrived != a.chunks - 1u) return;
+      if (arrived != a.chunks - 1u) {
+        FG_TRACE_FLUSH(a);
+        return;
+      }
     }
 
     // ---- last workgroup of the row: merge the other workgroups' lists ----
     const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
-    if (F::kTop && kk) {
+    if (F::kTop && fin_mode) {
+      // The finisher (at most 8 chunks): the others' lists are read until
+      // every entry is tagged, then placed in LDS beside its own and ranked
+      // by all four waves.  Their slots are cleared after the finish (a
+      // store here would hold the ranking behind the wait for its
+      // completion).
+      const uint32_t own = a.finisher - 1u;
+      const bool hi = lane >= 32u;
+      const uint32_t pos = lane & 31u;  // lanes 0-31: list 2t, 32-63: list 2t + 1
+      uint64_t x[4];
+      auto fetch = [&]() {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const uint32_t c = 2u * t + (hi ? 1u : 0u);
+          if (c != own && c < a.chunks && pos < kk)
+            x[t] = load_coherent(a.cand + (row_slot + c) * kMaxK + pos);
+        }
+      };
+#pragma unroll
+      for (int t = 0; t < 4; t++) x[t] = kListTag;
+      fetch();
+      FG_TRACE(a, 8);
+      for (uint32_t spin = 0;; spin++) {
+        bool miss = false;
+#pragma unroll
+        for (int t = 0; t < 4; t++) miss |= (x[t] & kListTag) == 0ull;
+        if (ballot(miss) == 0ull) break;
+        if (spin == kTagSpins) {  // never expected: the row reports an error
+#pragma unroll
+          for (int t = 0; t < 4; t++) x[t] = kListTag;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        fetch();
+      }
+      FG_TRACE(a, 4);
+      uint64_t* lists = &s_top[0][0];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint32_t c = 2u * t + (hi ? 1u : 0u);
+        if (c != own) lists[c * 32u + pos] = x[t] & ~kListTag;
+      }
+      if (lane < 32u) {
+        lists[own * 32u + lane] = lane < kk ? fin : 0ull;
+        s_rank[lane] = 0ull;
+      }
+      __syncthreads();
+      rank_place_lists(lists, 0u, kk, s_rank);
+      __syncthreads();
+      fin = lane < 32u ? s_rank[lane] : 0ull;
+      FG_TRACE(a, 5);
+    } else if (F::kTop && kk) {
       if (kk <= 32u) {
         // Lists of at most 32: two per register, the second loaded in
         // reverse into lanes 32-63, so a pair is already a bitonic sequence
@@ -1199,53 +1331,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
         uint64_t acc = 0ull;
         for (uint32_t c0 = 0; c0 < a.chunks; c0 += 8u) {
           uint64_t x[4];
-          if (fin_mode) {
-            // The finisher (at most 8 chunks): its own list from registers
-            // (reversed in the high lanes), the others' read until every
-            // entry is tagged, then cleared.
-            const uint32_t own = a.finisher - 1u;
-            // (past kk a list is not exact: those positions count as empty)
-            const uint64_t rev = lane_reverse64(fin);
-            const uint64_t mine = (pos < kk ? (hi ? rev : fin) : 0ull) | kListTag;
-            auto fetch = [&]() {
 #pragma unroll
-              for (int t = 0; t < 4; t++) {
-                const uint32_t c = 2u * t + (hi ? 1u : 0u);
-                if (c != own && c < a.chunks && pos < kk)
-                  x[t] = load_coherent(a.cand + (row_slot + c) * kMaxK + pos);
-              }
-            };
-#pragma unroll
-            for (int t = 0; t < 4; t++) x[t] = 2u * t + (hi ? 1u : 0u) == own ? mine : kListTag;
-            fetch();
-            for (uint32_t spin = 0;; spin++) {
-              bool miss = false;
-#pragma unroll
-              for (int t = 0; t < 4; t++) miss |= (x[t] & kListTag) == 0ull;
-              if (ballot(miss) == 0ull) break;
-              if (spin == kTagSpins) {  // never expected: the row reports an error
-#pragma unroll
-                for (int t = 0; t < 4; t++) x[t] = kListTag;
-                break;
-              }
-              __builtin_amdgcn_s_sleep(1);
-              fetch();
-            }
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-              x[t] &= ~kListTag;
-              const uint32_t c = 2u * t + (hi ? 1u : 0u);
-              if (c != own && c < a.chunks && pos < kk)
-                store_coherent(a.cand + (row_slot + c) * kMaxK + pos, uint64_t{0});
-            }
-          } else {
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-              const uint32_t c = c0 + 2u * t + (hi ? 1u : 0u);
-              x[t] = (c < a.chunks && pos < kk)
-                         ? load_coherent(a.cand + (row_slot + c) * kMaxK + pos)
-                         : 0ull;
-            }
+          for (int t = 0; t < 4; t++) {
+            const uint32_t c = c0 + 2u * t + (hi ? 1u : 0u);
+            x[t] = (c < a.chunks && pos < kk)
+                       ? load_coherent(a.cand + (row_slot + c) * kMaxK + pos)
+                       : 0ull;
           }
           if (spec && c0 == 0u) {
             // The waves' speculative keys travel with the first lists (the
@@ -1323,7 +1414,21 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   FG_TRACE(a, 6);
   finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
   if (a.chunks != 1u && !fin_mode && lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
+  if (a.chunks != 1u && fin_mode) {
+    // The finisher clears the other chunks' list slots it read (in the lane
+    // layout of its reads) for the next launch.
+    const bool hi = lane >= 32u;
+    const uint32_t pos = hi ? 63u - lane : lane;
+    const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const uint32_t c = 2u * t + (hi ? 1u : 0u);
+      if (c != a.finisher - 1u && c < a.chunks && pos < kk)
+        store_coherent(a.cand + (row_slot + c) * kMaxK + pos, uint64_t{0});
+    }
+  }
   FG_TRACE(a, 7);
+  FG_TRACE_FLUSH(a);
 }
 
 }  // namespace fg
