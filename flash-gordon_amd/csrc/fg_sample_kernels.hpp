@@ -1231,7 +1231,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (spec) ks0 = spec_key(a, row, lane, s_ks);
   } else if (fin_mode && chunk != a.finisher - 1u) {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
-    store_coherent(a.cand + slot * kMaxK + lane, lane < kk ? fin | kListTag : uint64_t{0});
+    if (lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin | kListTag);
     FG_TRACE(a, 3);
     FG_TRACE_FLUSH(a);
     return;
