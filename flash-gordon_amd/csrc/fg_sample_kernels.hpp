@@ -1227,6 +1227,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
   }
   uint32_t ks0 = 0u;
+  uint64_t* clear_at[4] = {nullptr, nullptr, nullptr, nullptr};  // the finisher's clearing stores
+  uint64_t clear_zero = 0ull;
+  asm volatile("" : "+v"(clear_zero));
   if (a.chunks == 1u) {  // the whole row is in this workgroup
     if (spec) ks0 = spec_key(a, row, lane, s_ks);
   } else if (fin_mode && chunk != a.finisher - 1u) {
@@ -1271,9 +1274,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (F::kTop && fin_mode) {
       // The finisher (at most 8 chunks): the others' lists are read until
       // every entry is tagged, then placed in LDS beside its own and ranked
-      // by all four waves.  Their slots are cleared after the finish (a
-      // store here would hold the ranking behind the wait for its
-      // completion).
+      // by all four waves.
       const uint32_t own = a.finisher - 1u;
       const bool hi = lane >= 32u;
       const uint32_t pos = lane & 31u;  // lanes 0-31: list 2t, 32-63: list 2t + 1
@@ -1313,6 +1314,18 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       if (lane < 32u) {
         lists[own * 32u + lane] = lane < kk ? fin : 0ull;
         s_rank[lane] = 0ull;
+      }
+      // The slots read are cleared for the next launch now, so the stores
+      // complete during the ranking and the finish (outstanding stores at
+      // the end would hold the kernel's completion).  Their address and
+      // data registers stay live to the end of the kernel (clear_keep):
+      // overwriting a register an outstanding store reads makes the
+      // compiler wait for the store.
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const uint32_t c = 2u * t + (hi ? 1u : 0u);
+        clear_at[t] = a.cand + (row_slot + c) * kMaxK + pos;
+        if (c != own && c < a.chunks && pos < kk) store_coherent(clear_at[t], clear_zero);
       }
       __syncthreads();
       rank_place_lists(lists, 0u, kk, s_rank);
@@ -1414,19 +1427,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   FG_TRACE(a, 6);
   finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
   if (a.chunks != 1u && !fin_mode && lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
-  if (a.chunks != 1u && fin_mode) {
-    // The finisher clears the other chunks' list slots it read (in the lane
-    // layout of its reads) for the next launch.
-    const bool hi = lane >= 32u;
-    const uint32_t pos = hi ? 63u - lane : lane;
-    const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const uint32_t c = 2u * t + (hi ? 1u : 0u);
-      if (c != a.finisher - 1u && c < a.chunks && pos < kk)
-        store_coherent(a.cand + (row_slot + c) * kMaxK + pos, uint64_t{0});
-    }
-  }
+  if (fin_mode)
+    asm volatile("" ::"v"(clear_at[0]), "v"(clear_at[1]), "v"(clear_at[2]), "v"(clear_at[3]),
+                 "v"(clear_zero));
   FG_TRACE(a, 7);
   FG_TRACE_FLUSH(a);
 }
