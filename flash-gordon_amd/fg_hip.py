@@ -485,6 +485,32 @@ class HipSampler:
         _check(self._lib.fg_sampler_hip_sample(self.handle, C.byref(b), _stream(stream),
                                                C.byref(err)), err)
 
+    def prepare(self, logits, uniforms, tokens, counts=None, token_logits=None, row_status=None,
+                penalised=None, logprobs=0, logprob_values=None, logprob_ids=None, rows=None,
+                logits_stride=None, counts_stride=None):
+        """The batch of a later sample() call marshalled once: returns a
+        function of the stream that launches it (for loops over fixed
+        buffers, where the per-call argument marshalling would dominate the
+        host's part)."""
+        rows = rows if rows is not None else logits.shape[0]
+        b = Batch(
+            _ptr(logits), logits_stride if logits_stride is not None else logits.stride(0),
+            _ptr(counts), (counts_stride if counts_stride is not None
+                           else (counts.stride(0) if counts is not None else 0)),
+            _ptr(uniforms), rows, _ptr(tokens), _ptr(token_logits), _ptr(row_status),
+            _ptr(penalised), logprobs, _ptr(logprob_values), _ptr(logprob_ids))
+        err = FgError()
+        bref, eref, fn, h = C.byref(b), C.byref(err), self._lib.fg_sampler_hip_sample, self.handle
+
+        def launch(stream=None):
+            status = fn(h, bref, _stream(stream), eref)
+            if status:
+                _check(status, err)
+
+        launch.keep = (b, err, logits, uniforms, tokens, counts, token_logits, row_status,
+                       penalised, logprob_values, logprob_ids)
+        return launch
+
     def history_increment(self, counts, tokens, row_status=None, rows=None, stream=None):
         rows = rows if rows is not None else tokens.numel()
         err = FgError()

@@ -580,3 +580,28 @@ def test_graph_replays_match_eager(dev, nucleus):
         assert np.array_equal(tok.cpu().numpy().view(np.uint32), eager["token"]), replay
         assert np.array_equal(tl.cpu().numpy().view(np.uint32), eager["logit"].view(np.uint32)), replay
         assert np.array_equal(st.cpu().numpy(), eager["status"]), replay
+
+
+def test_prepared_launch_matches_sample(dev):
+    """HipSampler.prepare (the batch marshalled once, launched per call)
+    gives the oracle's tokens, call after call on the same buffers."""
+    import torch
+    w = W.config2(rows=8)
+    s = fg_hip.HipSampler(W.V, 8)
+    s.set_configs([fg_hip.make_config(c["temperature"], c["top_p"], c["top_k"], c["presence"],
+                                      c["frequency"], c["repetition"]) for c in w["configs"]])
+    d_logits = to_dev(w["logits"], dev)
+    d_counts = to_dev(w["counts"], dev)
+    d_u = to_dev(w["uniforms"], dev)
+    tok = torch.full((8,), -1, dtype=torch.int32, device=dev)
+    st = torch.full((8,), -7, dtype=torch.int32, device=dev)
+    launch = s.prepare(d_logits, d_u, tok, counts=d_counts, row_status=st)
+    ref = W.oracle_run(w)
+    for _ in range(3):
+        tok.fill_(-1)
+        launch()
+        torch.cuda.synchronize()
+        got = tok.cpu().numpy().view(np.uint32)
+        assert np.array_equal(st.cpu().numpy(), ref["status"])
+        ok = ref["margin"] >= BOUNDARY
+        assert np.array_equal(got[ok], ref["token"][ok])
