@@ -494,13 +494,14 @@ def test_paired_layout_shares(dev, monkeypatch, groups, share, k):
 
 @pytest.mark.parametrize("groups,finisher,k", [(32, "1", 20), (32, "2", 32), (64, "3", 1),
                                                (128, "1", 20), (128, "6", 32), (128, "8", 7),
-                                               (128, "0", 20)])
+                                               (128, "0", 20), (256, "1", 20), (256, "1", 32)])
 def test_finisher_rows(dev, monkeypatch, groups, finisher, k):
     """The finisher hand-off (one chunk of each row reads the others' tagged
     lists; FG_HIP_FINISHER=c+1 picks chunk c, 0 the last-arriver hand-off):
     16 rows over 2, 4 or 8 chunks, finishing chunks whose list sits in the
     low or the high (reversed) lanes, top values at slice edges and in one
-    slice; three calls on one sampler with new inputs each (the finisher
+    slice (16 chunks: more than the finisher takes, so the last-arriver
+    hand-off runs, with the workgroups' rank merges); three calls on one sampler with new inputs each (the finisher
     clears the lists it reads, so a call sees none of the last one's).
     Exact against the oracle."""
     monkeypatch.setenv("FG_HIP_TARGET_GROUPS", str(groups))
