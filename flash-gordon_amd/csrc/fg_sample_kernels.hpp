@@ -509,11 +509,16 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
           const double draw = static_cast<double>(u) * tsum;
           const uint64_t hit2 = ballot(lane < cutoff && draw < tcum);
           const uint32_t pick = hit2 ? static_cast<uint32_t>(__builtin_ctzll(hit2)) : cutoff - 1u;
-          token = comp_id(readlane64(sorted, pick));
-          // The logit keeps its sign of zero: read it from the key-order list.
-          const uint64_t owner = ballot(fin != 0ull && comp_id(fin) == token);
-          token_logit = key_to_float(
-              comp_key(readlane64(fin, static_cast<uint32_t>(__builtin_ctzll(owner)))));
+          const uint64_t picked = readlane64(sorted, pick);
+          token = comp_id(picked);
+          if (comp_key(picked) != 0x80000000u) {
+            token_logit = key_to_float(comp_key(picked));  // the value's own key
+          } else {
+            // A zero keeps its sign: read it from the key-order list.
+            const uint64_t owner = ballot(fin != 0ull && comp_id(fin) == token);
+            token_logit = key_to_float(
+                comp_key(readlane64(fin, static_cast<uint32_t>(__builtin_ctzll(owner)))));
+          }
         }
       }
     }
