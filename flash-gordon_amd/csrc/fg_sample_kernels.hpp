@@ -1185,6 +1185,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const bool fin_mode = F::kTop && !F::kSpec && !F::kLse && !F::kNuc && a.finisher != 0u &&
                         !greedy && kk != 0u && kk <= 32u && a.chunks <= 8u;
   const bool fin_wg = fin_mode && a.chunks != 1u && chunk == a.finisher - 1u;
+  // The same for batches of greedy rows (no log-probs) over 2-64 chunks:
+  // one composite per chunk.
+  const bool gfin_mode = F::kGreedy && a.finisher != 0u && greedy && L == 0u && a.chunks >= 2u &&
+                         a.chunks <= static_cast<uint32_t>(kWave);
   // Lists of at most 32: the four waves rank their own entries.
   const bool rank_wg = F::kTop && kk != 0u && kk <= 32u;
   if (F::kTop) s_top[wave][lane] = mine;
@@ -1237,15 +1241,18 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   asm volatile("" : "+v"(clear_zero));
   if (a.chunks == 1u) {  // the whole row is in this workgroup
     if (spec) ks0 = spec_key(a, row, lane, s_ks);
-  } else if (fin_mode && chunk != a.finisher - 1u) {
+  } else if ((fin_mode || gfin_mode) && chunk != a.finisher - 1u) {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
-    if (lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin | kListTag);
+    if (fin_mode && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin | kListTag);
+    // A greedy composite is never 1 (its high word is a float key, at least
+    // 0x00800000, or 0 for none): 1 stands for "arrived, nothing here".
+    if (gfin_mode && lane == 0) store_coherent(a.greedy + slot, g != 0ull ? g : uint64_t{1});
     FG_TRACE(a, 3);
     FG_TRACE_FLUSH(a);
     return;
   } else {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
-    if (!fin_mode) {
+    if (!fin_mode && !gfin_mode) {
       // Publish the workgroup's partials with device-coherent stores.
       if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin);
       if (spec && lane < static_cast<uint32_t>(kWaves))
@@ -1405,11 +1412,36 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       FG_TRACE(a, 5);
     }
     if (F::kGreedy && greedy) {
-      for (uint32_t i = lane; i < a.chunks; i += kWave) {
-        const uint64_t x = load_coherent(a.greedy + row_slot + i);
-        g = x > g ? x : g;
+      if (gfin_mode) {
+        // The greedy finisher (at most 64 chunks, one per lane): the others'
+        // composites are read until every one has arrived (nonzero), their
+        // slots cleared for the next launch (early, as the list finisher's).
+        const uint32_t own = a.finisher - 1u;
+        const bool other = lane < a.chunks && lane != own;
+        uint64_t* const at = a.greedy + row_slot + lane;
+        uint64_t x = other ? 0ull : uint64_t{1};
+        if (other) x = load_coherent(at);
+        for (uint32_t spin = 0; ballot(x == 0ull) != 0ull; spin++) {
+          if (spin == kTagSpins) {  // never expected: the row reports an error
+            x = 1ull;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          if (x == 0ull) x = load_coherent(at);
+        }
+        clear_at[0] = at;
+        if (other) store_coherent(at, clear_zero);
+        const uint64_t xv = x == uint64_t{1} ? uint64_t{0} : x;
+        g = wave_max_u64(xv > g ? xv : g);
+      } else {
+        for (uint32_t i = lane; i < a.chunks; i += kWave) {
+          const uint64_t x = load_coherent(a.greedy + row_slot + i);
+          g = x > g ? x : g;
+          // Cleared for a greedy finisher in a later launch.
+          store_coherent(a.greedy + row_slot + i, uint64_t{0});
+        }
+        g = wave_max_u64(g);
       }
-      g = wave_max_u64(g);
     }
     if (lse) {
       double lm = -INFINITY, lz = 0.0;
@@ -1432,7 +1464,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   FG_TRACE(a, 6);
   finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
   if (a.chunks != 1u && !fin_mode && lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
-  if (fin_mode)
+  if (fin_mode || gfin_mode)
     asm volatile("" ::"v"(clear_at[0]), "v"(clear_at[1]), "v"(clear_at[2]), "v"(clear_at[3]),
                  "v"(clear_zero));
   FG_TRACE(a, 7);

@@ -392,10 +392,15 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
   a.split = geo.split;
   {
     // Finisher protocol (see the kernel): every row a top list of at most 32
-    // (no greedy row, no log-probs) over 2-8 chunks.
+    // (no greedy row, no log-probs) over 2-8 chunks, or every row greedy (no
+    // log-probs) over 2-64 chunks.
     bool ok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= 8u && b->logprobs == 0u;
     for (uint32_t r = 0; ok && r < b->rows; r++)
       ok = h_params[r].temperature > 0.0f && h_params[r].top_k >= 1u && h_params[r].top_k <= 32u;
+    bool gok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= fg::kMaxChunks &&
+               b->logprobs == 0u;
+    for (uint32_t r = 0; gok && r < b->rows; r++) gok = h_params[r].temperature == 0.0f;
+    ok = ok || gok;
     const uint32_t which = w.tuning.finisher > 0 ? static_cast<uint32_t>(w.tuning.finisher) - 1u : 0u;
     a.finisher = ok && which < chunks ? which + 1u : 0u;
   }
@@ -841,6 +846,8 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   // The finisher protocol needs cleared lists (the finisher clears what it reads).
   if (e == hipSuccess) e = hipMemset(s->ws.cand, 0, sizeof(uint64_t) * slots * fg::kMaxK);
   if (e == hipSuccess) e = hipMalloc(&s->ws.greedy, sizeof(uint64_t) * slots);
+  // So does the greedy finisher (a zero slot: not arrived).
+  if (e == hipSuccess) e = hipMemset(s->ws.greedy, 0, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.spec, sizeof(uint32_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.lse, sizeof(double) * slots * 2);
   if (e == hipSuccess) e = hipMalloc(&s->ws.zsum, sizeof(double) * slots * 3);

@@ -544,6 +544,36 @@ def test_finisher_and_last_arriver_calls_alternate(dev):
         check(w, run_hip(w, dev, sampler=s), W.oracle_run(w), f"alternating call {call}")
 
 
+@pytest.mark.parametrize("groups", [32, 128, 1024])
+def test_greedy_finisher_alternates_with_last_arriver(dev, monkeypatch, groups):
+    """The greedy finisher (batches of greedy rows: one chunk reads the
+    others' composites until all have arrived, then clears them) on 2, 8 and
+    64 chunks per row, alternating on one sampler with calls whose batch
+    mixes in a top-k row (the last-arriver hand-off, which reads the greedy
+    slots too and clears them).  Non-finite values win and fail their row
+    (src/output.c:560-599), ties go to the lower id; exact against the
+    oracle."""
+    monkeypatch.setenv("FG_HIP_TARGET_GROUPS", str(groups))
+    rows = 16
+    s = fg_hip.HipSampler(W.V, rows)
+    for call in range(6):
+        rng = np.random.default_rng(31 * groups + call)
+        logits = rng.normal(0, 3, (rows, W.V)).astype(np.float32)
+        logits[1, 77_777] = np.nan
+        logits[2, 150_000] = np.inf
+        logits[3, [5, 140_000]] = 30.0  # a tie across chunks
+        logits[4, :] = -1.0  # every value tied: id 0
+        counts = np.zeros((rows, W.V), dtype=np.uint32)
+        counts[6, rng.integers(0, W.V, 64)] = 1
+        configs = [W.cfg(0.0, 1.0, 1, repetition=1.05 if r == 6 else 1.0) for r in range(rows)]
+        if call % 2 == 1:
+            configs[9] = W.cfg(0.7, 0.9, 5)  # a top-k row: the last-arriver hand-off
+        w = dict(logits=logits, counts=counts, configs=configs,
+                 uniforms=rng.random(rows).astype(np.float32), logprobs=0)
+        check(w, run_hip(w, dev, sampler=s), W.oracle_run(w),
+              f"greedy finisher groups={groups} call={call}")
+
+
 @pytest.mark.parametrize("nucleus", [False, True])
 def test_graph_replays_match_eager(dev, nucleus):
     """One sample call captured in a HIP graph (the launch allocates and
