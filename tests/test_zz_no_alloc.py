@@ -60,7 +60,12 @@ def test_static_matches_sampler_two_calls(dev):
     # Call 2: fewer rows, whole-row nucleus controls (a second kernel on the
     # same stream), after call 1 left its contents in the array.
     w2 = W.config3(rows=24)
-    for k, (w, flags) in enumerate([(w1, 0), (w2, fg_hip.ALLOW_FULL_VOCAB)]):
+    # Calls 3 and 4: batches that take the finisher hand-offs (top-k 20 rows
+    # only; greedy rows only), after the calls above left their contents.
+    w3 = W.config2(rows=16)
+    w4 = W.config2(rows=8)
+    w4["configs"] = [W.cfg(0.0, 1.0, 1, presence=1.5, repetition=1.05)] * 8
+    for k, (w, flags) in enumerate([(w1, 0), (w2, fg_hip.ALLOW_FULL_VOCAB), (w3, 0), (w4, 0)]):
         got = _run(dev, w, flags, static=True)
         want = _run(dev, w, flags, static=False)
         _same(got, want, f"call {k + 1}")
