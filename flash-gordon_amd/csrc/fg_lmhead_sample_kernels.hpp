@@ -48,10 +48,10 @@ struct LmWork {
   unsigned long long* keys;   // [2][line] greedy composites, zero between launches
   uint32_t* arrivals;         // [2][line] greedy arrivals, zero between launches
   // sampled tokens, token-major (zero between launches where noted)
-  uint64_t* wg_lists;         // [2][wg_cap][kMaxK]
+  uint64_t* wg_lists;         // [2][grp_cap][kMaxK][kLmGroup] (position-major per group)
   uint32_t* wg_count;         // [2][wg_cap]
   uint32_t* grp_arrivals;     // [2][grp_cap][line], zero between launches
-  uint64_t* grp_lists;        // [2][grp_cap][kMaxK] each group's best kk
+  uint64_t* grp_lists;        // [2][kMaxK][grp_cap] each group's best kk (position-major)
   uint32_t* grp_count;        // [2][grp_cap]
   uint32_t* fin_arrivals;     // [2][line], zero between launches
   unsigned long long* bound;  // [2][line] best group kk-th so far, zero between launches
@@ -86,9 +86,9 @@ __device__ __forceinline__ RowParams lm_params(const LmSampleArgs& s, uint32_t t
 constexpr uint32_t kLmAhead = 16;
 constexpr uint32_t kNoList = 0xffffffffu;  // lm_merge: skip nothing
 constexpr uint32_t kLmStage = 3u * kWave;  // < 64 left + one round of 64, spare slots
-__device__ __forceinline__ uint64_t lm_merge(const uint64_t* lists, const uint32_t* cnt,
-                                             uint32_t nl, uint32_t kk, uint32_t skip,
-                                             uint64_t floor, uint64_t* buf) {
+__device__ __forceinline__ uint64_t lm_merge(const uint64_t* lists, uint32_t es,
+                                             const uint32_t* cnt, uint32_t nl, uint32_t kk,
+                                             uint32_t skip, uint64_t floor, uint64_t* buf) {
   const uint32_t lane = lane_id();
   // Entries below floor (a lower bound of the row's kk-th) cannot enter.
   const uint64_t R0 = floor > kFiniteComp ? floor - 1ull : kFiniteComp - 1ull;
@@ -96,17 +96,18 @@ __device__ __forceinline__ uint64_t lm_merge(const uint64_t* lists, const uint32
   for (uint32_t l0 = 0; l0 < nl; l0 += kWave) {
     const uint32_t l = l0 + lane;
     const bool use = l < nl && l != skip;
-    const uint64_t* mine = lists + static_cast<uint64_t>(l) * kMaxK;
+    const uint64_t* mine = lists + l;  // entry j at mine + j * es
     uint32_t c = use ? load_coherent(cnt + l) : 0u;
     uint64_t head[kLmAhead];
 #pragma unroll
-    for (uint32_t j = 0; j < kLmAhead; j++) head[j] = use ? load_coherent(mine + j) : 0ull;
+    for (uint32_t j = 0; j < kLmAhead; j++)
+      head[j] = use ? load_coherent(mine + static_cast<uint64_t>(j) * es) : 0ull;
     c = c < kk ? c : kk;
     for (uint32_t j = 0; ballot(j < c) != 0ull; j++) {
       uint64_t x = 0ull;
 #pragma unroll
       for (uint32_t q = 0; q < kLmAhead; q++) x = q == j ? head[q] : x;
-      if (j >= kLmAhead && j < c) x = load_coherent(mine + j);
+      if (j >= kLmAhead && j < c) x = load_coherent(mine + static_cast<uint64_t>(j) * es);
       const bool beats = j < c && x > t.R;
       if (!beats) c = j;  // sorted: the rest of this list cannot enter either
       top_stage(t, beats ? x : 0ull);
@@ -118,14 +119,33 @@ __device__ __forceinline__ uint64_t lm_merge(const uint64_t* lists, const uint32
 }
 
 #ifdef FG_LM_TRACE
-// Phase timestamps of trace builds: [workgroup][8] (s_memrealtime, 100 MHz).
+// Phase timestamps of trace builds: [workgroup][8] (s_memrealtime, 100 MHz),
+// kept in LDS and copied out where the workgroup's work ends (FG_LMT_FLUSH):
+// a global store per stamp would make the compiler wait for its completion
+// before reusing its registers.
 __device__ uint64_t g_lm_trace[8192 * 8];
-#define FG_LMT(slot)                                                                 \
-  do {                                                                               \
-    if (lane_id() == 0) g_lm_trace[blockIdx.x * 8u + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+__shared__ uint64_t s_lm_trace[8];
+#define FG_LMT(slot)                                                      \
+  do {                                                                    \
+    if (lane_id() == 0) s_lm_trace[slot] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define FG_LMT_INIT                                                       \
+  do {                                                                    \
+    if (threadIdx.x < 8u) s_lm_trace[threadIdx.x] = 0ull;                 \
+  } while (0)
+#define FG_LMT_FLUSH                                                      \
+  do {                                                                    \
+    if (lane_id() == 0)                                                   \
+      for (int i_ = 0; i_ < 8; i_++) g_lm_trace[blockIdx.x * 8u + i_] = s_lm_trace[i_]; \
   } while (0)
 #else
 #define FG_LMT(slot) \
+  do {               \
+  } while (0)
+#define FG_LMT_INIT \
+  do {              \
+  } while (0)
+#define FG_LMT_FLUSH \
   do {               \
   } while (0)
 #endif
@@ -180,6 +200,7 @@ __global__ __launch_bounds__(kDenseBlock) void dense_q8_sample_kernel(LmSampleAr
   __shared__ uint64_t s_cand[B][kLmCand];
   __shared__ uint64_t s_best[kDenseBlock / kWave][B];
   __shared__ uint64_t s_stage[B][kLmStage];
+  FG_LMT_INIT;
   if (threadIdx.x == 0) FG_LMT(0);
   stage_inputs<B>(a, s_x);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -258,7 +279,12 @@ __global__ __launch_bounds__(kDenseBlock) void dense_q8_sample_kernel(LmSampleAr
   const uint64_t sorted = wave_sort_desc(s_cand[t][lane]);
   const uint32_t n = static_cast<uint32_t>(__popcll(ballot(lane < kk && sorted != 0ull)));
   const uint64_t slot = static_cast<uint64_t>(t) * w.wg_cap + blockIdx.x;
-  if (lane < n) store_coherent(w.wg_lists + slot * kMaxK + lane, sorted);
+  // Position-major within the group: the merging workgroup's loads of one
+  // position of all 64 lists are one contiguous 512-byte run.
+  if (lane < n)
+    store_coherent(w.wg_lists + ((static_cast<uint64_t>(t) * w.grp_cap + grp) * kMaxK + lane) *
+                                    kLmGroup + blockIdx.x % kLmGroup,
+                   sorted);
   if (lane == 0) store_coherent(w.wg_count + slot, n);
   wait_memory();  // hand-off ordering: see wait_memory()
   uint32_t arrived = 0u;
@@ -268,7 +294,10 @@ __global__ __launch_bounds__(kDenseBlock) void dense_q8_sample_kernel(LmSampleAr
                                      __HIP_MEMORY_SCOPE_AGENT);
   arrived = __builtin_amdgcn_readfirstlane(arrived);
   if (t == 0) FG_LMT(2);
-  if (arrived + 1u != grp_size) return;
+  if (arrived + 1u != grp_size) {
+    if (t == 0) FG_LMT_FLUSH;
+    return;
+  }
 
   // Group: merge its workgroups' lists.  When every other group has
   // counted in already, this group is the token's last: it merges the
@@ -277,23 +306,24 @@ __global__ __launch_bounds__(kDenseBlock) void dense_q8_sample_kernel(LmSampleAr
   const uint32_t groups_in =
       __builtin_amdgcn_readfirstlane(load_coherent(w.fin_arrivals + t * kLineWords));
   const uint64_t wslot = static_cast<uint64_t>(t) * w.wg_cap + grp * kLmGroup;
-  const uint64_t* grp_lists = w.grp_lists + static_cast<uint64_t>(t) * w.grp_cap * kMaxK;
+  const uint64_t* grp_lists = w.grp_lists + static_cast<uint64_t>(t) * kMaxK * w.grp_cap;
   const uint32_t* grp_count = w.grp_count + static_cast<uint64_t>(t) * w.grp_cap;
   const bool last_group = groups_in + 1u == ngroups;
   // The row's kk-th is at or above every finished group's kk-th.
   unsigned long long* bound = w.bound + t * kLmLine64;
   const uint64_t floor_g =
       __hip_atomic_load(bound, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  uint64_t fin = lm_merge(w.wg_lists + wslot * kMaxK, w.wg_count + wslot, grp_size, kk, kNoList,
-                          floor_g, s_stage[t]);
+  uint64_t fin = lm_merge(w.wg_lists + (static_cast<uint64_t>(t) * w.grp_cap + grp) * kMaxK * kLmGroup,
+                          kLmGroup, w.wg_count + wslot, grp_size, kk, kNoList, floor_g, s_stage[t]);
   if (last_group)
-    fin = wave_merge_desc(fin, lm_merge(grp_lists, grp_count, ngroups, kk,
+    fin = wave_merge_desc(fin, lm_merge(grp_lists, w.grp_cap, grp_count, ngroups, kk,
                                         static_cast<uint32_t>(grp), floor_g, s_stage[t]));
   fin = lane < kk ? fin : 0ull;
   if (t == 0) FG_LMT(3);
   if (!last_group) {
     const uint32_t gn = static_cast<uint32_t>(__popcll(ballot(fin != 0ull)));
-    if (lane < gn) store_coherent(w.grp_lists + gslot * kMaxK + lane, fin);
+    if (lane < gn)
+      store_coherent(w.grp_lists + (static_cast<uint64_t>(t) * kMaxK + lane) * w.grp_cap + grp, fin);
     const uint64_t kth = readlane64(fin, kk - 1u);
     if (lane == 0) {
       store_coherent(w.grp_count + gslot, gn);
@@ -308,10 +338,13 @@ __global__ __launch_bounds__(kDenseBlock) void dense_q8_sample_kernel(LmSampleAr
                                        __HIP_MEMORY_SCOPE_AGENT);
     arrived = __builtin_amdgcn_readfirstlane(arrived);
     if (t == 0) FG_LMT(4);
-    if (arrived + 1u != ngroups) return;
+    if (arrived + 1u != ngroups) {
+      if (t == 0) FG_LMT_FLUSH;
+      return;
+    }
     // Token: the last group to count in merges the groups' lists.
     const uint64_t floor_t = __hip_atomic_load(bound, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    fin = lm_merge(grp_lists, grp_count, ngroups, kk, kNoList, floor_t, s_stage[t]);
+    fin = lm_merge(grp_lists, w.grp_cap, grp_count, ngroups, kk, kNoList, floor_t, s_stage[t]);
   }
   if (lane == 0) {
     store_coherent(w.fin_arrivals + t * kLineWords, 0u);
@@ -327,6 +360,7 @@ __global__ __launch_bounds__(kDenseBlock) void dense_q8_sample_kernel(LmSampleAr
   finish_row(fa, p, tok, fin, 0ull, -INFINITY, 0.0, Mass{-INFINITY, 0.0, 0.0}, nullptr, nullptr,
              pen, s.uniforms[tok], 1.0 / static_cast<double>(p.temperature));
   if (t == 0) FG_LMT(6);
+  if (t == 0) FG_LMT_FLUSH;
 }
 
 }  // namespace fg

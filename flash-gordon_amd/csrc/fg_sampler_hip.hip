@@ -567,7 +567,7 @@ fg_status fg_hip_output_slice_create(fg_hip_output_slice** out, uint32_t vocab, 
     // Two tokens per pass: lists of every workgroup and every group.
     s->wg_cap = dense_groups(rows);
     s->grp_cap = (s->wg_cap + fg::kLmGroup - 1u) / fg::kLmGroup;
-    const size_t wl = sizeof(uint64_t) * 2u * s->wg_cap * fg::kMaxK;
+    const size_t wl = sizeof(uint64_t) * 2u * s->grp_cap * fg::kMaxK * fg::kLmGroup;
     if (e == hipSuccess) e = hipMalloc(&s->d_wg_lists, wl);
     if (e == hipSuccess) e = hipMalloc(&s->d_wg_count, sizeof(uint32_t) * 2u * s->wg_cap);
     // Counters and running values, one 128-byte line each, then the running
