@@ -1330,9 +1330,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       // The slots read are cleared for the next launch now, so the stores
       // complete during the ranking and the finish (outstanding stores at
       // the end would hold the kernel's completion).  Their address and
-      // data registers stay live to the end of the kernel (clear_keep):
-      // overwriting a register an outstanding store reads makes the
-      // compiler wait for the store.
+      // data registers stay live to the end of the kernel (the empty asm
+      // statement that uses clear_at and clear_zero there): overwriting a
+      // register an outstanding store reads makes the compiler wait for the
+      // store.
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const uint32_t c = 2u * t + (hi ? 1u : 0u);
