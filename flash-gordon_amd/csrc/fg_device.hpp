@@ -443,6 +443,18 @@ __device__ __forceinline__ double wave_prefix_sum_f64(double x) {
   return x + before;
 }
 
+// The same scan where lanes 32-63 hold zeros: exact in lanes 0-31 (the
+// upper lanes' results are not meaningful).
+__device__ __forceinline__ double wave_prefix_sum_f64_lo32(double x) {
+  x += row_shr_f64<1>(x);
+  x += row_shr_f64<2>(x);
+  x += row_shr_f64<4>(x);
+  x += row_shr_f64<8>(x);
+  const double r0 = __longlong_as_double(static_cast<long long>(
+      readlane64(static_cast<uint64_t>(__double_as_longlong(x)), 15)));
+  return (lane_id() >> 4) == 1u ? x + r0 : x;
+}
+
 // The same scan for u32 counts.
 __device__ __forceinline__ uint32_t wave_prefix_sum_u32(uint32_t x) {
   x += row_shr<1>(x);

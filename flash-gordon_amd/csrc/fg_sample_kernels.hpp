@@ -511,8 +511,16 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
       const double d = live ? v - vmax : -INFINITY;
       const double e = exp(d);
       const double te = exp(d * inv_t);
-      const double ecum = wave_prefix_sum_f64(e);
-      const double tcum = wave_prefix_sum_f64(te);
+      // Lists of at most 32 (every top-k up to 32) have no terms past lane
+      // 31: the scans over two rows of 16 skip the upper rows' offsets.
+      double ecum, tcum;
+      if (topk <= 32u) {
+        ecum = wave_prefix_sum_f64_lo32(e);
+        tcum = wave_prefix_sum_f64_lo32(te);
+      } else {
+        ecum = wave_prefix_sum_f64(e);
+        tcum = wave_prefix_sum_f64(te);
+      }
       double sum = __longlong_as_double(static_cast<long long>(
           readlane64(static_cast<uint64_t>(__double_as_longlong(ecum)), limit - 1u)));
       // Relative error bound of the f32-term mass (see Mass).
@@ -1275,7 +1283,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     }
   }
   for (int w = 0; w < kWaves; w++) {
-    g = s_greedy[w] > g ? s_greedy[w] : g;
+    if (F::kGreedy) g = s_greedy[w] > g ? s_greedy[w] : g;  // no greedy row: g stays 0
     if (lse) lse_accumulate(m, z, s_lm[w], s_lz[w], t_eff);
     if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
   }
