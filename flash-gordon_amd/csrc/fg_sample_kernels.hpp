@@ -1246,13 +1246,18 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   if (F::kTop) s_top[wave][lane] = mine;
   if (F::kTop && rank_wg && wave == 0 && lane < 32u) s_rank[lane] = 0ull;
   if (lane == 0) {
-    s_greedy[wave] = gbest;
+    // Only the partials some row of the launch reads.
+    if (F::kGreedy) s_greedy[wave] = gbest;
     if (F::kSpec) s_ks[wave] = st.KS;
-    s_lm[wave] = wm;
-    s_lz[wave] = wz;
-    s_nm[wave] = wmass.m;
-    s_nz[wave] = wmass.z;
-    s_ne[wave] = wmass.e;
+    if (F::kLse) {
+      s_lm[wave] = wm;
+      s_lz[wave] = wz;
+    }
+    if (F::kNuc) {
+      s_nm[wave] = wmass.m;
+      s_nz[wave] = wmass.z;
+      s_ne[wave] = wmass.e;
+    }
   }
   __syncthreads();
   if (F::kTop && rank_wg) {
