@@ -78,8 +78,10 @@ struct SampleArgs {
   uint32_t split;         // chunks [0, split) run in the grid's first half, the
                           // rest in its second half (split == chunks: one layout)
   uint32_t logprobs;
-  uint32_t finisher;      // c + 1: chunk c finishes each row (tagged lists, no
-                          // counter); 0: the last arriver does
+  uint32_t finisher;      // bits 0-7: c + 1, chunk c finishes each row (tagged
+                          // words, no counter), 0 the last arriver does; bits
+                          // 16-28: the launch's epoch (1..kMaxEpoch)
+  uint32_t wait_ticks;    // finisher hand-off: wait limit, s_memrealtime ticks
   uint32_t* tokens;
   float* token_logits;
   int32_t* row_status;
@@ -1009,14 +1011,77 @@ __device__ inline uint64_t spec_check(const SampleArgs& a, const RowParams& p, u
   return fin;
 }
 
-// ---- the finisher's tagged lists ----------------------------------------------
+// ---- the finisher's tagged words ---------------------------------------------
+//
+// In the finisher hand-off the other chunks' lists (and greedy composites)
+// travel as self-describing words: bit 63 set, bits 62-50 the launch's epoch
+// (1-8191, advanced by the host every launch), bits 49-0 the payload,
+// key << 18 | (2^18 - 1 - id) (larger payload = larger key, then lower id:
+// the ladder's order; greedy words carry greedy_comp's high word as the
+// key), 0 for an empty entry.  The finisher reads a word until it carries
+// this launch's epoch, so slots are never cleared and a word stored late, by
+// a launch whose finisher gave up, is never read as a later launch's; the
+// host clears the workspace when the epoch wraps.  Ids must be below 2^18
+// (larger vocabularies take the last-arriver hand-off).  A finisher that has
+// not seen every word after the launch's wait limit (a.wait_ticks of the
+// 100 MHz clock) reports kStTimeout for its row instead of a token.
+constexpr uint32_t kWireIdBits = 18;
+constexpr uint32_t kWireVocab = 1u << kWireIdBits;  // ids below this travel in a word
+constexpr uint64_t kWirePayload = (1ull << 50) - 1ull;
+constexpr uint32_t kMaxEpoch = 8191;  // epochs 1..8191
+constexpr int32_t kStTimeout = 7;     // FG_ERR_UNAVAILABLE: the finisher's wait gave up
 
-// Bit 63 is free in a composite (key << 31 | id part): set on a published
-// entry, so the finisher tells a stored entry from the cleared slot (0).
-constexpr uint64_t kListTag = 1ull << 63;
-// Polls before the finisher gives up on a list (about 30 ms); the row then
-// has no candidates and reports an error rather than waiting without end.
-constexpr uint32_t kTagSpins = 1u << 20;
+__device__ __forceinline__ uint64_t wire_header(uint32_t epoch) {
+  return (0x2000ull | epoch) << 50;
+}
+__device__ __forceinline__ bool wire_current(uint64_t w, uint64_t header) {
+  return (w >> 50) == (header >> 50);
+}
+// Payload of a composite (make_comp order); 0 stays 0.
+__device__ __forceinline__ uint64_t wire_payload(uint64_t comp) {
+  if (comp == 0ull) return 0ull;
+  return (static_cast<uint64_t>(comp_key(comp)) << kWireIdBits) |
+         static_cast<uint64_t>(kWireVocab - 1u - comp_id(comp));
+}
+__device__ __forceinline__ uint64_t comp_of_payload(uint64_t w) {
+  if (w == 0ull) return 0ull;
+  return make_comp(static_cast<uint32_t>(w >> kWireIdBits),
+                   kWireVocab - 1u - static_cast<uint32_t>(w & (kWireVocab - 1u)));
+}
+// Greedy composite <-> payload (high word = greedy key, low word = ~id).
+__device__ __forceinline__ uint64_t greedy_payload(uint64_t g) {
+  if (g == 0ull) return 0ull;
+  return ((g >> 32) << kWireIdBits) | static_cast<uint64_t>(kWireVocab - 1u - greedy_id(g));
+}
+__device__ __forceinline__ uint64_t greedy_of_payload(uint64_t w) {
+  if (w == 0ull) return 0ull;
+  const uint32_t id = kWireVocab - 1u - static_cast<uint32_t>(w & (kWireVocab - 1u));
+  return ((w >> kWireIdBits) << 32) | static_cast<uint64_t>(~id);
+}
+
+// c + 1 when chunk c finishes each row (finisher hand-off), else 0.
+__device__ __forceinline__ uint32_t finisher_of(const SampleArgs& a) { return a.finisher & 0xffu; }
+
+// Whether the finisher's wait has passed its limit, at poll `spin` (0, 1,
+// ...) of a wait whose first clock reading goes to t0.  The clock (a scalar
+// memory read) is read at the first poll and every 32nd after it; a limit
+// of 0 gives up at the first poll.
+__device__ __forceinline__ bool wait_passed(const SampleArgs& a, uint32_t spin, uint64_t& t0) {
+  if (a.wait_ticks == 0u) return true;
+  if (spin % 32u) return false;
+  const uint64_t now = __builtin_amdgcn_s_memrealtime();
+  if (spin == 0u) t0 = now;
+  return now - t0 > a.wait_ticks;
+}
+
+// The row's outputs when its finisher gave up waiting.
+__device__ inline void timeout_row(const SampleArgs& a, uint32_t row) {
+  if (lane_id() == 0u) {
+    a.tokens[row] = kInvalidId;
+    if (a.token_logits) a.token_logits[row] = -INFINITY;
+    if (a.row_status) a.row_status[row] = kStTimeout;
+  }
+}
 
 // ---- merging by rank ----------------------------------------------------------
 //
@@ -1234,13 +1299,13 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   // giving chunk 0 a longer slice, so that it would usually end last, cost
   // more stream time than the wait it saved).  All four waves of the
   // finishing workgroup rank the lists.
-  const bool fin_mode = F::kTop && !F::kSpec && !F::kLse && !F::kNuc && a.finisher != 0u &&
+  const bool fin_mode = F::kTop && !F::kSpec && !F::kLse && !F::kNuc && finisher_of(a) != 0u &&
                         !greedy && kk != 0u && kk <= 32u && a.chunks <= 8u;
-  const bool fin_wg = fin_mode && a.chunks != 1u && chunk == a.finisher - 1u;
+  const bool fin_wg = fin_mode && a.chunks != 1u && chunk == finisher_of(a) - 1u;
   // The same for batches of greedy rows (no log-probs) over 2-64 chunks:
   // one composite per chunk.
-  const bool gfin_mode = F::kGreedy && a.finisher != 0u && greedy && L == 0u && a.chunks >= 2u &&
-                         a.chunks <= static_cast<uint32_t>(kWave);
+  const bool gfin_mode = F::kGreedy && finisher_of(a) != 0u && greedy && L == 0u &&
+                         a.chunks >= 2u && a.chunks <= static_cast<uint32_t>(kWave);
   // Lists of at most 32: the four waves rank their own entries.
   const bool rank_wg = F::kTop && kk != 0u && kk <= 32u;
   if (F::kTop) s_top[wave][lane] = mine;
@@ -1293,17 +1358,15 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (F::kNuc && nuc) mass_accumulate(zs, s_nm[w], s_nz[w], s_ne[w]);
   }
   uint32_t ks0 = 0u;
-  uint64_t* clear_at[4] = {nullptr, nullptr, nullptr, nullptr};  // the finisher's clearing stores
-  uint64_t clear_zero = 0ull;
-  asm volatile("" : "+v"(clear_zero));
+  bool gave_up = false;  // the finisher's wait passed its limit
   if (a.chunks == 1u) {  // the whole row is in this workgroup
     if (spec) ks0 = spec_key(a, row, lane, s_ks);
-  } else if ((fin_mode || gfin_mode) && chunk != a.finisher - 1u) {
+  } else if ((fin_mode || gfin_mode) && chunk != finisher_of(a) - 1u) {
     const uint64_t slot = static_cast<uint64_t>(row) * a.chunks + chunk;
-    if (fin_mode && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin | kListTag);
-    // A greedy composite is never 1 (its high word is a float key, at least
-    // 0x00800000, or 0 for none): 1 stands for "arrived, nothing here".
-    if (gfin_mode && lane == 0) store_coherent(a.greedy + slot, g != 0ull ? g : uint64_t{1});
+    const uint64_t header = wire_header(a.finisher >> 16u);
+    if (fin_mode && lane < kk)
+      store_coherent(a.cand + slot * kMaxK + lane, header | wire_payload(fin));
+    if (gfin_mode && lane == 0) store_coherent(a.greedy + slot, header | greedy_payload(g));
     FG_TRACE(a, 3);
     FG_TRACE_FLUSH(a);
     return;
@@ -1342,9 +1405,11 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     const uint64_t row_slot = static_cast<uint64_t>(row) * a.chunks;
     if (F::kTop && fin_mode) {
       // The finisher (at most 8 chunks): the others' lists are read until
-      // every entry is tagged, then placed in LDS beside its own and ranked
-      // by all four waves.
-      const uint32_t own = a.finisher - 1u;
+      // every entry carries this launch's epoch, then placed in LDS beside
+      // its own and ranked by all four waves (which meet at the barriers
+      // below even when the wait gives up).
+      const uint32_t own = finisher_of(a) - 1u;
+      const uint64_t header = wire_header(a.finisher >> 16u);
       const bool hi = lane >= 32u;
       const uint32_t pos = lane & 31u;  // lanes 0-31: list 2t, 32-63: list 2t + 1
       uint64_t x[4];
@@ -1357,17 +1422,17 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
         }
       };
 #pragma unroll
-      for (int t = 0; t < 4; t++) x[t] = kListTag;
+      for (int t = 0; t < 4; t++) x[t] = header;
       fetch();
       FG_TRACE(a, 8);
+      uint64_t t0 = 0ull;
       for (uint32_t spin = 0;; spin++) {
         bool miss = false;
 #pragma unroll
-        for (int t = 0; t < 4; t++) miss |= (x[t] & kListTag) == 0ull;
+        for (int t = 0; t < 4; t++) miss |= !wire_current(x[t], header);
         if (ballot(miss) == 0ull) break;
-        if (spin == kTagSpins) {  // never expected: the row reports an error
-#pragma unroll
-          for (int t = 0; t < 4; t++) x[t] = kListTag;
+        if (wait_passed(a, spin, t0)) {
+          gave_up = true;
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -1378,24 +1443,11 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const uint32_t c = 2u * t + (hi ? 1u : 0u);
-        if (c != own) lists[c * 32u + pos] = x[t] & ~kListTag;
+        if (c != own) lists[c * 32u + pos] = comp_of_payload(x[t] & kWirePayload);
       }
       if (lane < 32u) {
         lists[own * 32u + lane] = lane < kk ? fin : 0ull;
         s_rank[lane] = 0ull;
-      }
-      // The slots read are cleared for the next launch now, so the stores
-      // complete during the ranking and the finish (outstanding stores at
-      // the end would hold the kernel's completion).  Their address and
-      // data registers stay live to the end of the kernel (the empty asm
-      // statement that uses clear_at and clear_zero there): overwriting a
-      // register an outstanding store reads makes the compiler wait for the
-      // store.
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const uint32_t c = 2u * t + (hi ? 1u : 0u);
-        clear_at[t] = a.cand + (row_slot + c) * kMaxK + pos;
-        if (c != own && c < a.chunks && pos < kk) store_coherent(clear_at[t], clear_zero);
       }
       __syncthreads();
       rank_place_lists(lists, 0u, kk, s_rank);
@@ -1472,30 +1524,29 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     if (F::kGreedy && greedy) {
       if (gfin_mode) {
         // The greedy finisher (at most 64 chunks, one per lane): the others'
-        // composites are read until every one has arrived (nonzero), their
-        // slots cleared for the next launch (early, as the list finisher's).
-        const uint32_t own = a.finisher - 1u;
+        // words are read until every one carries this launch's epoch.
+        const uint32_t own = finisher_of(a) - 1u;
+        const uint64_t header = wire_header(a.finisher >> 16u);
         const bool other = lane < a.chunks && lane != own;
-        uint64_t* const at = a.greedy + row_slot + lane;
-        uint64_t x = other ? 0ull : uint64_t{1};
-        if (other) x = load_coherent(at);
-        for (uint32_t spin = 0; ballot(x == 0ull) != 0ull; spin++) {
-          if (spin == kTagSpins) {  // never expected: the row reports an error
-            x = 1ull;
+        const uint64_t* const at = a.greedy + row_slot + lane;
+        uint64_t x = other ? load_coherent(at) : header;
+        uint64_t t0 = 0ull;
+        for (uint32_t spin = 0; ballot(!wire_current(x, header)) != 0ull; spin++) {
+          if (wait_passed(a, spin, t0)) {
+            gave_up = true;
             break;
           }
           __builtin_amdgcn_s_sleep(1);
-          if (x == 0ull) x = load_coherent(at);
+          if (!wire_current(x, header)) x = load_coherent(at);
         }
-        clear_at[0] = at;
-        if (other) store_coherent(at, clear_zero);
-        const uint64_t xv = x == uint64_t{1} ? uint64_t{0} : x;
+        const uint64_t xv = greedy_of_payload(x & kWirePayload);
         g = wave_max_u64(xv > g ? xv : g);
       } else {
         for (uint32_t i = lane; i < a.chunks; i += kWave) {
           const uint64_t x = load_coherent(a.greedy + row_slot + i);
           g = x > g ? x : g;
-          // Cleared for a greedy finisher in a later launch.
+          // Cleared: a greedy finisher of a later launch must never find an
+          // untagged composite here (its high bits could read as a tag).
           store_coherent(a.greedy + row_slot + i, uint64_t{0});
         }
         g = wave_max_u64(g);
@@ -1520,11 +1571,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   // One copy of the check and of the finish serves both paths.
   if (spec) fin = spec_check(a, p, row, pen, lrow, crow, fin, kk, s_ks, ks0, s_buf[0], &s_wg_key);
   FG_TRACE(a, 6);
-  finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
-  if (a.chunks != 1u && !fin_mode && lane == 0) store_coherent(&a.row_done[row * kLineWords], 0u);
-  if (fin_mode || gfin_mode)
-    asm volatile("" ::"v"(clear_at[0]), "v"(clear_at[1]), "v"(clear_at[2]), "v"(clear_at[3]),
-                 "v"(clear_zero));
+  if (gave_up)
+    timeout_row(a, row);
+  else
+    finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
+  if (a.chunks != 1u && !fin_mode && !gfin_mode && lane == 0)
+    store_coherent(&a.row_done[row * kLineWords], 0u);
   FG_TRACE(a, 7);
   FG_TRACE_FLUSH(a);
 }

@@ -79,6 +79,43 @@ const SampleLaunch* const kVecLaunch =
 const SampleLaunch kScalarLaunch =
     launch_sample<fg::Features<false, true, true, true, true, true, true>>;
 
+// The same instantiations as kernel symbols (occupancy queries), index 64
+// the scalar one.
+template <int kBits>
+const void* vec_kernel() {
+  return reinterpret_cast<const void*>(
+      &fg::sample_rows_kernel<fg::Features<true, (kBits & 1) != 0, (kBits & 2) != 0,
+                                           (kBits & 4) != 0, (kBits & 8) != 0, (kBits & 16) != 0,
+                                           (kBits & 4) != 0 && (kBits & 32) != 0>>);
+}
+template <int... kBits>
+const void* kernel_of(int index) {
+  static const void* const table[sizeof...(kBits)] = {vec_kernel<kBits>()...};
+  return table[index];
+}
+const void* sample_kernel(int index) {
+  if (index >= 64)
+    return reinterpret_cast<const void*>(
+        &fg::sample_rows_kernel<fg::Features<false, true, true, true, true, true, true>>);
+  return kernel_of<0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21,
+                   22, 23, 24, 25, 26, 27, 28, 29, 30, 31, 32, 33, 34, 35, 36, 37, 38, 39, 40, 41,
+                   42, 43, 44, 45, 46, 47, 48, 49, 50, 51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61,
+                   62, 63>(index);
+}
+
+// Workgroups of one instantiation that a CU holds at once (0: unknown),
+// queried once per process: every GPU this library runs on is a gfx950.
+std::atomic<int> g_occupancy[65];
+int occupancy(int index) {
+  int n = g_occupancy[index].load(std::memory_order_relaxed);
+  if (n) return n;
+  const void* k = sample_kernel(index);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, fg::kBlock, 0) != hipSuccess || n < 0)
+    n = 0;
+  g_occupancy[index].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 // ---- Q8_0 cooked matrix-vector launch shapes
 
 constexpr uint32_t kDensePassTokens = 2;  // tokens per pass over the weights
@@ -147,6 +184,7 @@ struct Tuning {
   int32_t paired = -1;           // FG_HIP_PAIRED (0 / 1)
   int32_t pace = -1;             // FG_HIP_PACE (0 / 1)
   int32_t finisher = -1;         // FG_HIP_FINISHER (0: off, c + 1: chunk c finishes)
+  uint64_t wait_us = 100000u;    // FG_HIP_FINISHER_WAIT_US: the finisher's wait limit
 };
 Tuning tuning_from_env() {
   Tuning t;
@@ -161,6 +199,10 @@ Tuning tuning_from_env() {
   if (const char* v = getenv("FG_HIP_PAIRED")) t.paired = atoi(v) != 0;
   if (const char* v = getenv("FG_HIP_PACE")) t.pace = atoi(v) != 0;
   if (const char* v = getenv("FG_HIP_FINISHER")) t.finisher = atoi(v);  // 0: off, c + 1: chunk c
+  if (const char* v = getenv("FG_HIP_FINISHER_WAIT_US")) {
+    const long long x = strtoll(v, nullptr, 10);
+    if (x >= 0 && x <= 60000000) t.wait_us = static_cast<uint64_t>(x);
+  }
   return t;
 }
 
@@ -237,6 +279,8 @@ struct Workspace {
   uint32_t* nuc_deep;       // [max_rows]
   float* nuc_max;           // [max_rows]
   uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
+  uint32_t* epoch;          // host: the last finisher launch's epoch (0: none yet)
+  uint32_t cus;             // compute units of the device (co-residency check)
   Tuning tuning;            // environment overrides
 };
 
@@ -247,6 +291,7 @@ struct fg_sampler_hip {
   RowParams* h_params;      // host mirror of the uploaded table (launch-variant choice)
   uint32_t config_rows;     // rows configured by the last set_configs
   uint64_t* counters;       // event counters, FG_SAMPLE_TRACE builds only
+  uint32_t epoch;           // the last finisher launch's epoch (Workspace::epoch)
 };
 
 namespace {
@@ -287,8 +332,11 @@ static_assert(kStaticBytes == FG_SAMPLER_HIP_STATIC_BYTES, "header size out of d
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
 
 constexpr int kStaticMaxDevices = 64;
-// Per device: the address of its copy of `scratch` (0 until first use).
+// Per device: the address of its copy of `scratch` (0 until first use), and
+// the last finisher epoch used on it (calls that overlap on one device race,
+// as they do on the array itself).
 std::atomic<uintptr_t> g_scratch_addr[kStaticMaxDevices];
+uint32_t g_static_epoch[kStaticMaxDevices];
 
 hipError_t static_workspace(Workspace* w) {
   int dev = 0;
@@ -317,7 +365,19 @@ hipError_t static_workspace(Workspace* w) {
   w->nuc_deep = reinterpret_cast<uint32_t*>(p + kOffDeep);
   w->nuc_max = reinterpret_cast<float*>(p + kOffNucMax);
   w->trace = nullptr;
-  w->tuning = tuning_from_env();
+  w->epoch = &g_static_epoch[dev];
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  w->cus = static_cast<uint32_t>(cus);
+  // The environment is read once per process; the array holds kMaxGroups
+  // workgroups' slots beyond the rows, so a larger target is clamped.
+  static const Tuning tuning = [] {
+    Tuning t = tuning_from_env();
+    if (t.target_groups > fg::kMaxGroups) t.target_groups = fg::kMaxGroups;
+    return t;
+  }();
+  w->tuning = tuning;
   return hipSuccess;
 }
 
@@ -352,6 +412,33 @@ hipError_t fill_params(const Workspace& w, const RowParams* h, uint32_t rows, hi
     params_fill_kernel<<<1, kParamsPerFill, 0, stream>>>(p, w.params, w.row_done);
   }
   return hipGetLastError();
+}
+
+// Returns the workspace's hand-off slots to zero (when the finisher epoch
+// wraps, so that no word of an earlier launch can carry the new one).
+__global__ void __launch_bounds__(256)
+    epoch_clear_kernel(uint64_t* cand, uint64_t cand_words, uint64_t* greedy, uint64_t slots) {
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < cand_words;
+       i += stride) {
+    cand[i] = 0ull;
+    if (i < slots) greedy[i] = 0ull;
+  }
+}
+
+// The next finisher epoch (1..kMaxEpoch); on a wrap the workspace is
+// cleared first, on the same stream.
+hipError_t next_epoch(const Workspace& w, hipStream_t stream, uint32_t* epoch) {
+  uint32_t e = *w.epoch + 1u;
+  if (e > fg::kMaxEpoch) {
+    epoch_clear_kernel<<<256, 256, 0, stream>>>(w.cand, w.slots * fg::kMaxK, w.greedy, w.slots);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    e = 1u;
+  }
+  *w.epoch = e;
+  *epoch = e;
+  return hipSuccess;
 }
 
 // One fused sampling launch (two with whole-row nucleus rows) over a batch
@@ -390,19 +477,21 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
   a.wave_elems = geo.wave_elems;
   a.wave_elems_b = geo.wave_elems_b;
   a.split = geo.split;
+  uint32_t finisher = 0u;
   {
     // Finisher protocol (see the kernel): every row a top list of at most 32
     // (no greedy row, no log-probs) over 2-8 chunks, or every row greedy (no
-    // log-probs) over 2-64 chunks.
-    bool ok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= 8u && b->logprobs == 0u;
+    // log-probs) over 2-64 chunks; ids that fit a tagged word.
+    bool ok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= 8u && b->logprobs == 0u &&
+              vocab <= fg::kWireVocab;
     for (uint32_t r = 0; ok && r < b->rows; r++)
       ok = h_params[r].temperature > 0.0f && h_params[r].top_k >= 1u && h_params[r].top_k <= 32u;
     bool gok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= fg::kMaxChunks &&
-               b->logprobs == 0u;
+               b->logprobs == 0u && vocab <= fg::kWireVocab;
     for (uint32_t r = 0; gok && r < b->rows; r++) gok = h_params[r].temperature == 0.0f;
     ok = ok || gok;
     const uint32_t which = w.tuning.finisher > 0 ? static_cast<uint32_t>(w.tuning.finisher) - 1u : 0u;
-    a.finisher = ok && which < chunks ? which + 1u : 0u;
+    finisher = ok && which < chunks ? which + 1u : 0u;
   }
   a.pace = geo.pace;
   a.logprobs = b->logprobs;
@@ -446,6 +535,19 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
   const int bits = (any_pen ? 1 : 0) | (any_greedy ? 2 : 0) | (any_top ? 4 : 0) |
                    (b->logprobs ? 8 : 0) | (any_nuc ? 16 : 0) | (any_spec ? 32 : 0);
   const uint32_t grid = b->rows * chunks;
+  // The finisher waits for the other workgroups of its row: only when the
+  // whole grid fits on the device at once (occupancy x CUs) is every one of
+  // them sure to run while it waits.  Otherwise the last arriver finishes.
+  if (finisher && static_cast<uint64_t>(grid) <=
+                      static_cast<uint64_t>(occupancy(vec ? bits : 64)) * w.cus) {
+    uint32_t epoch = 0u;
+    const hipError_t e = next_epoch(w, stream, &epoch);
+    if (e != hipSuccess) return hip_fail(err, e, "sampler epoch");
+    a.finisher = finisher | epoch << 16;
+    // s_memrealtime runs at 100 MHz; limits up to 42.9 s fit.
+    const uint64_t ticks = w.tuning.wait_us * 100u;
+    a.wait_ticks = ticks < UINT32_MAX ? static_cast<uint32_t>(ticks) : UINT32_MAX;
+  }
   (vec ? kVecLaunch[bits] : kScalarLaunch)(grid, stream, a);
   // Whole-row nucleus rows whose cut lies past the kMaxK best are finished
   // by a second kernel; the others return at once.
@@ -719,14 +821,11 @@ fg_status fg_hip_output_slice_run_dense_sampled(
     a.d.tokens = tokens - t0 < kDensePassTokens ? tokens - t0 : kDensePassTokens;
     for (uint32_t t = 0; t < 2u; t++)
       a.p[t] = t < a.d.tokens ? row_params(&configs[t0 + t]) : RowParams{};
-    // The merges reuse the staged inputs' LDS: at least one TopList stage.
-    const size_t merge = sizeof(uint64_t) * (fg::kCap + fg::kWave);
+    // Dynamic LDS holds the staged inputs only (the merges use static arrays).
     if (a.d.tokens == 1u) {
-      const size_t lds = sizeof(float) * a.d.in > merge ? sizeof(float) * a.d.in : merge;
-      fg::dense_q8_sample_kernel<1><<<groups, fg::kDenseBlock, lds, st>>>(a);
+      fg::dense_q8_sample_kernel<1><<<groups, fg::kDenseBlock, sizeof(float) * a.d.in, st>>>(a);
     } else {
-      const size_t lds = sizeof(float) * a.d.in * 2u > merge ? sizeof(float) * a.d.in * 2u : merge;
-      fg::dense_q8_sample_kernel<2><<<groups, fg::kDenseBlock, lds, st>>>(a);
+      fg::dense_q8_sample_kernel<2><<<groups, fg::kDenseBlock, sizeof(float) * a.d.in * 2u, st>>>(a);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(err, e, "sampled output launch");
@@ -828,7 +927,11 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   s->vocab = vocab;
   s->ws.max_rows = max_rows;
   s->ws.tuning = tuning_from_env();
+  s->ws.epoch = &s->epoch;
   hipError_t e = hipGetDevice(&s->device);
+  int cus = 0;
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device);
+  s->ws.cus = static_cast<uint32_t>(cus);
   // rows * chunks(rows) <= max(target, kMaxGroups) + rows for every batch
   // size.
   const uint64_t groups_cap =
@@ -843,10 +946,9 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   }
   if (e == hipSuccess) e = hipMalloc(&s->ws.params, sizeof(RowParams) * max_rows);
   if (e == hipSuccess) e = hipMalloc(&s->ws.cand, sizeof(uint64_t) * slots * fg::kMaxK);
-  // The finisher protocol needs cleared lists (the finisher clears what it reads).
+  // Hand-off slots start cleared (no word carries an epoch yet).
   if (e == hipSuccess) e = hipMemset(s->ws.cand, 0, sizeof(uint64_t) * slots * fg::kMaxK);
   if (e == hipSuccess) e = hipMalloc(&s->ws.greedy, sizeof(uint64_t) * slots);
-  // So does the greedy finisher (a zero slot: not arrived).
   if (e == hipSuccess) e = hipMemset(s->ws.greedy, 0, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.spec, sizeof(uint32_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.lse, sizeof(double) * slots * 2);
@@ -888,6 +990,12 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   (void)hipFree(s->ws.trace);
   free(s->h_params);
   free(s);
+}
+
+fg_status fg_sampler_hip_set_wait_limit(fg_sampler_hip* s, uint64_t wait_us, fg_error* err) {
+  if (!s || wait_us > 60000000u) return arg_fail(err, "invalid finisher wait limit");
+  s->ws.tuning.wait_us = wait_us;
+  return FG_OK;
 }
 
 fg_status fg_sampler_hip_set_configs(fg_sampler_hip* s, const fg_sampler_config* configs,

@@ -41,6 +41,7 @@ EXPORTS = (
     "fg_output_history_decode", "fg_output_history_decode_vocab",
     "fg_sampler_hip_create", "fg_sampler_hip_destroy", "fg_sampler_hip_set_configs",
     "fg_sampler_hip_sample", "fg_sampler_hip_history_increment", "fg_sampler_hip_sample_static",
+    "fg_sampler_hip_set_wait_limit",
     "fg_output_better", "fg_output_combine", "fg_output_split_way_for_rank",
     "fg_output_split_rank", "fg_output_split_span", "fg_output_split_combine_finalists",
     "fg_hip_output_slice_create", "fg_hip_output_slice_destroy", "fg_hip_output_slice_ways",
@@ -159,6 +160,7 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_sampler_hip_sample_static":
             (C.c_int, [u32, C.POINTER(SamplerConfig), u32, C.POINTER(Batch), P, E]),
         "fg_sampler_hip_history_increment": (C.c_int, [P, P, u64, P, P, u32, P, E]),
+        "fg_sampler_hip_set_wait_limit": (C.c_int, [P, u64, E]),
         "fg_output_better": (C.c_bool, [f32, u32, f32, u32]),
         "fg_output_combine": (None, [f32, u32, f32, u32, C.POINTER(f32), C.POINTER(u32)]),
         "fg_output_split_way_for_rank": (C.c_bool, [u32, u32, C.POINTER(u32)]),
@@ -510,6 +512,11 @@ class HipSampler:
         launch.keep = (b, err, logits, uniforms, tokens, counts, token_logits, row_status,
                        penalised, logprob_values, logprob_ids)
         return launch
+
+    def set_wait_limit(self, wait_us: int):
+        """The collector hand-off's wait limit for later calls (microseconds)."""
+        err = FgError()
+        _check(self._lib.fg_sampler_hip_set_wait_limit(self.handle, wait_us, C.byref(err)), err)
 
     def history_increment(self, counts, tokens, row_status=None, rows=None, stream=None):
         rows = rows if rows is not None else tokens.numel()

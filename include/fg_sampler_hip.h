@@ -133,11 +133,22 @@ typedef struct fg_sampler_hip fg_sampler_hip;
  * call.  Allocates the device workspace once (candidate lists, row counters);
  * the calls below allocate nothing.  Uses the current HIP device.  Reads the
  * tuning variables FG_HIP_TARGET_GROUPS, FG_HIP_PAIRED, FG_HIP_FRONT_SHARE,
- * FG_HIP_PACE and FG_HIP_FINISHER (launch geometry and hand-off only;
- * results do not depend on them). */
+ * FG_HIP_PACE, FG_HIP_FINISHER and FG_HIP_FINISHER_WAIT_US (launch geometry
+ * and hand-off only; results do not depend on them). */
 fg_status fg_sampler_hip_create(fg_sampler_hip **out, uint32_t vocab, uint32_t max_rows,
                                 fg_error *err);
 void fg_sampler_hip_destroy(fg_sampler_hip *sampler);
+
+/* No counterpart in the reference (its per-token dispatches wait on a host
+ * fence, src/output.c:702-756): the wait limit of the finisher hand-off of
+ * later fg_sampler_hip_sample calls, in microseconds (default 100000).  In
+ * that hand-off one workgroup of each row waits, on the device, for the
+ * row's other workgroups (it is used only when the whole launch fits on the
+ * device at once); a row whose wait passes the limit gets row_status
+ * FG_ERR_UNAVAILABLE and token 0xffffffff instead of a token.  0 makes
+ * every such row that is not complete at the first look report it (a
+ * host-side way to exercise that path). */
+fg_status fg_sampler_hip_set_wait_limit(fg_sampler_hip *sampler, uint64_t wait_us, fg_error *err);
 
 /* Validates each row's controls as fg_sampler_config_validate does and copies
  * them to the device table used by later fg_sampler_hip_sample calls.  Row r

@@ -547,7 +547,7 @@ def test_finisher_and_last_arriver_calls_alternate(dev):
 @pytest.mark.parametrize("groups", [32, 128, 1024])
 def test_greedy_finisher_alternates_with_last_arriver(dev, monkeypatch, groups):
     """The greedy finisher (batches of greedy rows: one chunk reads the
-    others' composites until all have arrived, then clears them) on 2, 8 and
+    others' words until all carry the launch's epoch) on 2, 8 and
     64 chunks per row, alternating on one sampler with calls whose batch
     mixes in a top-k row (the last-arriver hand-off, which reads the greedy
     slots too and clears them).  Non-finite values win and fail their row
@@ -572,6 +572,69 @@ def test_greedy_finisher_alternates_with_last_arriver(dev, monkeypatch, groups):
                  uniforms=rng.random(rows).astype(np.float32), logprobs=0)
         check(w, run_hip(w, dev, sampler=s), W.oracle_run(w),
               f"greedy finisher groups={groups} call={call}")
+
+
+@pytest.mark.parametrize("greedy", [False, True])
+def test_finisher_wait_limit_reports_and_next_call_is_exact(dev, greedy):
+    """A finisher whose wait passes its limit reports FG_ERR_UNAVAILABLE (7)
+    and token 0xffffffff for its row instead of sampling from the lists it
+    has (forced from the host: a limit of 0 us gives up at the first look
+    unless every list is in).  The rows that finish are exact.  The other
+    workgroups never wait, so the launch completes either way; their lists
+    land after the finisher gave up, carrying that launch's epoch, and the
+    next calls (limit restored, new data) are exact."""
+    rows = 64
+    s = fg_hip.HipSampler(W.V, rows)
+    w = W.config2(rows=rows)
+    if greedy:
+        w["configs"] = [W.cfg(0.0, 1.0, 1, presence=1.5, repetition=1.05)] * rows
+    s.set_wait_limit(0)
+    got = run_hip(w, dev, sampler=s)
+    ref = W.oracle_run(w)
+    gave_up = got["status"] == 7
+    assert gave_up.any(), "a 0 us limit should give up on some row"
+    assert (got["token"][gave_up] == 0xFFFFFFFF).all()
+    done = ~gave_up
+    assert np.array_equal(got["status"][done], ref["status"][done])
+    ok = (got["token"][done] == ref["token"][done]) | (ref["margin"][done] < BOUNDARY)
+    assert ok.all(), "rows that finished under the limit differ from the oracle"
+    s.set_wait_limit(100000)
+    for call in range(2):
+        w2 = dict(w)
+        w2["logits"] = np.roll(w["logits"], 104_729 * (call + 1), axis=1)
+        check(w2, run_hip(w2, dev, sampler=s), W.oracle_run(w2), f"after the limit, call {call}")
+
+
+def test_finisher_epoch_wrap(dev, monkeypatch):
+    """The hand-off epoch runs 1..8191 and the workspace is cleared when it
+    wraps: 8,200 calls of a two-row batch on one sampler (eight chunks per
+    row, the finisher hand-off), the inputs changed before the first, the
+    wrapping and the last calls, each of those checked against the
+    oracle."""
+    import torch
+    monkeypatch.setenv("FG_HIP_TARGET_GROUPS", "16")
+    rows, vocab = 2, 8192
+    s = fg_hip.HipSampler(vocab, rows)
+    s.set_configs([fg_hip.make_config(0.9, 0.9, 16, 0.0, 0.0, 1.0)] * rows)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    checks = {0, 8189, 8190, 8191, 8192, 8199}
+    for call in range(8200):
+        if call in checks:
+            rng = np.random.default_rng(call)
+            w = dict(logits=rng.normal(0, 2, (rows, vocab)).astype(np.float32),
+                     counts=np.zeros((rows, vocab), dtype=np.uint32),
+                     configs=[W.cfg(0.9, 0.9, 16)] * rows,
+                     uniforms=rng.random(rows).astype(np.float32), logprobs=0)
+            x, u = to_dev(w["logits"], dev), to_dev(w["uniforms"], dev)
+        s.sample(x, u, tok, row_status=st)
+        if call in checks:
+            torch.cuda.synchronize()
+            got = dict(token=tok.cpu().numpy().view(np.uint32), status=st.cpu().numpy())
+            ref = W.oracle_run(w)
+            assert np.array_equal(got["status"], ref["status"]), f"call {call}"
+            ok = (got["token"] == ref["token"]) | (ref["margin"] < BOUNDARY)
+            assert ok.all(), f"call {call}: {got['token']} vs {ref['token']}"
 
 
 @pytest.mark.parametrize("nucleus", [False, True])
