@@ -441,7 +441,7 @@ __global__ void __launch_bounds__(kNucBlock) nucleus_rows_kernel(SampleArgs a) {
   __shared__ NucLds s;
   const uint32_t row = blockIdx.x;
   const uint32_t tid = threadIdx.x;
-  const RowParams p = a.params[row];
+  const RowParams p = row_controls(a, row);
   if (!(p.temperature > 0.0f) || p.top_k != 0u || a.nuc_deep[row] == 0u) return;
   const bool pen = (p.flags & kRowPenalties) && a.counts != nullptr;
   const float* lrow = a.logits + static_cast<uint64_t>(row) * a.lstride;

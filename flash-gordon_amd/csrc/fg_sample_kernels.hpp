@@ -62,13 +62,16 @@ constexpr int32_t kStFormat = 4;
 constexpr int32_t kStMismatch = 5;
 constexpr int32_t kStLimit = 8;  // whole-row nucleus cut deeper than the kMaxK best
 
+// Rows of controls a sampling launch can carry in its own arguments.
+constexpr uint32_t kInlineRows = 64;
+
 struct SampleArgs {
   const float* logits;
   uint64_t lstride;
   const uint32_t* counts;
   uint64_t cstride;
   const float* uniforms;
-  const RowParams* params;
+  RowParams* params;      // the device table of controls (read, or written from inline)
   uint32_t vocab;
   uint32_t rows;
   uint32_t chunks;      // workgroups per row
@@ -99,7 +102,47 @@ struct SampleArgs {
   uint32_t* nuc_deep;    // [rows] whole-row nucleus: 1 = cut deeper than the kMaxK best
   float* nuc_max;        // [rows] whole-row nucleus: the row's largest finite value
   uint64_t* trace;       // FG_SAMPLE_TRACE builds only: [workgroup][16] timestamps
+  // Controls carried by value (inline > 0): rows [0, inline) of the table,
+  // read from here and written to `params` by workgroup 0 for later
+  // launches that read the table.
+  uint32_t inline_rows;
+  RowParams row_inline[kInlineRows];
 };
+
+// Row r's controls (r wave-uniform), read with scalar loads from one place
+// or the other under a uniform branch.  A launch reads the table only when
+// it carries no controls of its own, so the table never changes while it is
+// read: it is read as constant memory (scalar loads, whatever the launch
+// stores elsewhere).  The empty asm keeps the two loads apart: merged into
+// one load from a selected address, the load would be a flat, per-lane one.
+typedef const __attribute__((address_space(4))) RowParams* ConstRowParams;
+__device__ __forceinline__ RowParams row_controls(const SampleArgs& a, uint32_t r) {
+  RowParams p;
+  if (a.inline_rows) {
+    p = a.row_inline[r];
+    asm volatile("" ::: "memory");
+  } else {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const ConstRowParams q = (ConstRowParams)(a.params) + r;
+    p.temperature = q->temperature;
+    p.top_p = q->top_p;
+    p.top_k = q->top_k;
+    p.presence = q->presence;
+    p.frequency = q->frequency;
+    p.repetition = q->repetition;
+    p.flags = q->flags;
+    p.reserved = q->reserved;
+#else
+    p = a.params[r];
+#endif
+  }
+  return p;
+}
+// Workgroup 0 of a launch with inline controls writes them to the table.
+__device__ __forceinline__ void store_inline_controls(const SampleArgs& a) {
+  if (a.inline_rows && blockIdx.x == 0u && threadIdx.x < a.inline_rows)
+    a.params[threadIdx.x] = a.row_inline[threadIdx.x];
+}
 
 // Phase timestamps (s_memrealtime, 100 MHz) for builds with FG_SAMPLE_TRACE;
 // compiled out otherwise.
@@ -1155,7 +1198,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   const uint32_t lane = lane_id();
   uint32_t row, chunk;
   block_row_chunk(blockIdx.x, a.rows, a.chunks, a.split, &row, &chunk);
-  const RowParams p = a.params[row];
+  const RowParams p = row_controls(a, row);
+  // After the read: a store to the table before it would keep the compiler
+  // from reading the table with scalar loads.
+  store_inline_controls(a);
   const float urow = a.uniforms[row];  // early: the row's last step needs it
   const bool greedy = p.temperature == 0.0f;
   const uint32_t L = a.logprobs;

@@ -292,6 +292,7 @@ struct fg_sampler_hip {
   uint32_t config_rows;     // rows configured by the last set_configs
   uint64_t* counters;       // event counters, FG_SAMPLE_TRACE builds only
   uint32_t epoch;           // the last finisher launch's epoch (Workspace::epoch)
+  bool params_dirty;        // h_params not yet in the device table
 };
 
 namespace {
@@ -443,10 +444,13 @@ hipError_t next_epoch(const Workspace& w, hipStream_t stream, uint32_t* epoch) {
 
 // One fused sampling launch (two with whole-row nucleus rows) over a batch
 // whose per-row controls are h_params on the host (variant and layout choice)
-// and w.params on the device.  The caller has checked the batch against
-// w.max_rows and the configured rows.
+// and w.params on the device, or, with inline_rows > 0, rows [0, inline_rows)
+// of h_params carried in the launch's arguments (and written to w.params by
+// the launch).  The caller has checked the batch against w.max_rows and the
+// configured rows.
 fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t vocab,
-                        const fg_sampler_hip_batch* b, hipStream_t stream, fg_error* err) {
+                        const fg_sampler_hip_batch* b, hipStream_t stream, uint32_t inline_rows,
+                        fg_error* err) {
   if (!b->logits || !b->tokens || !b->uniforms || !b->rows || b->rows > w.max_rows ||
       b->logits_stride < vocab || (b->counts && b->counts_stride < vocab) ||
       b->logprobs > fg::kMaxK || (b->logprobs && (!b->logprob_values || !b->logprob_ids)))
@@ -510,6 +514,8 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
   a.nuc_deep = w.nuc_deep;
   a.nuc_max = w.nuc_max;
   a.trace = w.trace;
+  a.inline_rows = inline_rows;
+  if (inline_rows) memcpy(a.row_inline, h_params, sizeof(RowParams) * inline_rows);
 
   // The vector path addresses a slice with 32-bit byte offsets.
   const bool vec = aligned16(b->logits) && (b->logits_stride % 4u) == 0u &&
@@ -1012,20 +1018,44 @@ fg_status fg_sampler_hip_set_configs(fg_sampler_hip* s, const fg_sampler_config*
   for (uint32_t r = 0; r < rows; r++) {
     s->h_params[r] = row_params(&configs[r]);
   }
-  // The controls reach the device table as arguments of fill kernels on
-  // `stream` (ordered after earlier launches that read the table and before
-  // later ones): no host copy, no staging buffer, nothing to wait for.
-  const hipError_t e = fill_params(s->ws, s->h_params, rows, as_stream(stream));
-  if (e != hipSuccess) return hip_fail(err, e, "upload sampler configuration");
+  // The controls travel with the next launch that reads them: in the
+  // arguments of the next sample (batches of up to fg::kInlineRows
+  // configured rows), else as arguments of fill kernels launched first on
+  // that call's stream.  No host copy, no staging buffer, nothing to wait
+  // for, and no launch of its own.
+  (void)stream;
   s->config_rows = rows;
+  s->params_dirty = true;
   return FG_OK;
 }
+
+namespace {
+// Brings the device table up to date on `stream` with fill kernels.
+fg_status flush_params(fg_sampler_hip* s, hipStream_t stream, fg_error* err) {
+  if (!s->params_dirty) return FG_OK;
+  const hipError_t e = fill_params(s->ws, s->h_params, s->config_rows, stream);
+  if (e != hipSuccess) return hip_fail(err, e, "upload sampler configuration");
+  s->params_dirty = false;
+  return FG_OK;
+}
+}  // namespace
 
 fg_status fg_sampler_hip_sample(fg_sampler_hip* s, const fg_sampler_hip_batch* b, void* stream,
                                 fg_error* err) {
   if (!s || !b || b->rows > s->config_rows)
     return arg_fail(err, "invalid sampled output arguments");
-  return sample_launch(s->ws, s->h_params, s->vocab, b, as_stream(stream), err);
+  // Fresh controls ride in this launch's arguments when they fit.
+  uint32_t inline_rows = 0u;
+  if (s->params_dirty && s->config_rows <= fg::kInlineRows) {
+    inline_rows = s->config_rows;
+  } else {
+    const fg_status st = flush_params(s, as_stream(stream), err);
+    if (st != FG_OK) return st;
+  }
+  const fg_status st =
+      sample_launch(s->ws, s->h_params, s->vocab, b, as_stream(stream), inline_rows, err);
+  if (st == FG_OK) s->params_dirty = false;
+  return st;
 }
 
 fg_status fg_sampler_hip_sample_static(uint32_t vocab, const fg_sampler_config* configs,
@@ -1050,10 +1080,15 @@ fg_status fg_sampler_hip_sample_static(uint32_t vocab, const fg_sampler_config* 
   Workspace w;
   hipError_t e = static_workspace(&w);
   if (e != hipSuccess) return hip_fail(err, e, "static sampler workspace");
-  // Controls by value through kernel arguments (fill kernels).
-  e = fill_params(w, h, b->rows, as_stream(stream));
-  if (e != hipSuccess) return hip_fail(err, e, "static sampler controls");
-  return sample_launch(w, h, vocab, b, as_stream(stream), err);
+  // Controls by value: in the sampling launch's own arguments when they fit,
+  // else as arguments of fill kernels launched first.
+  uint32_t inline_rows = b->rows;
+  if (b->rows > fg::kInlineRows) {
+    e = fill_params(w, h, b->rows, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(err, e, "static sampler controls");
+    inline_rows = 0u;
+  }
+  return sample_launch(w, h, vocab, b, as_stream(stream), inline_rows, err);
 }
 
 fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
@@ -1062,6 +1097,8 @@ fg_status fg_sampler_hip_history_increment(fg_sampler_hip* s, uint32_t* counts,
                                            fg_error* err) {
   if (!s || !counts || !tokens || !rows || rows > s->config_rows || counts_stride < s->vocab)
     return arg_fail(err, "invalid output history token");
+  const fg_status st = flush_params(s, as_stream(stream), err);
+  if (st != FG_OK) return st;
   fg::history_increment_kernel<<<(rows + 255u) / 256u, 256, 0, as_stream(stream)>>>(
       counts, counts_stride, s->vocab, tokens, row_status,
       reinterpret_cast<const uint32_t*>(s->ws.params) + offsetof(RowParams, flags) / 4u,

@@ -514,7 +514,7 @@ class HipSampler:
         return launch
 
     def set_wait_limit(self, wait_us: int):
-        """The collector hand-off's wait limit for later calls (microseconds)."""
+        """The finisher hand-off's wait limit for later calls (microseconds)."""
         err = FgError()
         _check(self._lib.fg_sampler_hip_set_wait_limit(self.handle, wait_us, C.byref(err)), err)
 

@@ -150,15 +150,18 @@ void fg_sampler_hip_destroy(fg_sampler_hip *sampler);
  * host-side way to exercise that path). */
 fg_status fg_sampler_hip_set_wait_limit(fg_sampler_hip *sampler, uint64_t wait_us, fg_error *err);
 
-/* Validates each row's controls as fg_sampler_config_validate does and copies
- * them to the device table used by later fg_sampler_hip_sample calls.  Row r
- * of a batch uses configs[r].  Stream-ordered and asynchronous: the controls
- * travel as the arguments of small fill kernels launched on `stream` (64
- * rows each), so the call never waits for the device and needs no staging
- * copy.  The reference ships these controls with every token
- * (src/protocol.c:1158-1166); an owner loop may call this before every
- * sample.  Launches that read the table (sample, history_increment) must be
- * on the same stream. */
+/* Validates each row's controls as fg_sampler_config_validate does and keeps
+ * them for later fg_sampler_hip_sample calls.  Row r of a batch uses
+ * configs[r].  Launches nothing itself: up to 64 configured rows travel in
+ * the arguments of the next sample launch (which also writes them to the
+ * sampler's device table), more as the arguments of small fill kernels
+ * launched first by the next call that reads the controls (sample or
+ * history_increment), on that call's stream.  So the call never waits for
+ * the device, needs no staging copy, and an owner loop that sets every
+ * row's controls before every sample, as the reference ships them with
+ * every token (src/protocol.c:1158-1166), costs one launch per step.
+ * `stream` is unused (kept for the signature); launches that read the
+ * controls must be on one stream. */
 fg_status fg_sampler_hip_set_configs(fg_sampler_hip *sampler, const fg_sampler_config *configs,
                                      uint32_t rows, uint32_t flags, void *stream,
                                      fg_error *err);

@@ -197,6 +197,40 @@ def test_owner_loop_controls_change_every_call(dev):
         check(w, got, W.oracle_run(w, threads=cores()), f"owner call {i}")
 
 
+def test_controls_reach_the_table_for_later_calls(dev):
+    """set_configs launches nothing: up to 64 configured rows travel in the
+    next sample's arguments (which also writes them to the device table),
+    more go by fill kernels first.  A smaller batch after set_configs, then
+    the full batch again with no set_configs in between (read from the
+    table), then 80 rows (fill kernels): each call matches the oracle with
+    the controls last set."""
+    for rows in (64, 80):
+        w = W.config2(rows=rows)
+        for r in range(0, rows, 5):
+            w["configs"][r] = W.cfg(0.0, 1.0, 1, repetition=1.1)  # greedy rows mixed in
+        s = fg_hip.HipSampler(W.V, rows)
+        s.set_configs([fg_hip.make_config(c["temperature"], c["top_p"], c["top_k"], c["presence"],
+                                          c["frequency"], c["repetition"]) for c in w["configs"]])
+        half = dict(w, logits=w["logits"][:16], counts=w["counts"][:16],
+                    configs=w["configs"][:16], uniforms=w["uniforms"][:16])
+        check(half, run_hip_configured(half, dev, s), W.oracle_run(half), f"{rows}: first 16 rows")
+        check(w, run_hip_configured(w, dev, s), W.oracle_run(w), f"{rows}: all rows, from the table")
+
+
+def run_hip_configured(w, dev, s):
+    """run_hip on a sampler whose controls are already set (no set_configs)."""
+    import torch
+    rows = w["logits"].shape[0]
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    tl = torch.empty(rows, dtype=torch.float32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    s.sample(to_dev(np.ascontiguousarray(w["logits"]), dev), to_dev(w["uniforms"], dev), tok,
+             counts=to_dev(np.ascontiguousarray(w["counts"]), dev), token_logits=tl, row_status=st)
+    torch.cuda.synchronize()
+    return dict(token=tok.cpu().numpy().view(np.uint32), logit=tl.cpu().numpy(),
+                status=st.cpu().numpy())
+
+
 def test_mixed_rows_and_greedy_logprobs(dev):
     """Greedy, sampled and unpenalised rows in one batch, with log-probs."""
     w = W.config2(rows=12)
