@@ -1,17 +1,22 @@
-// gfx950 kernel for whole-row nucleus rows (top_k 0) whose top-p cut lies
-// deeper than the 64 best logits that the fused pass keeps.
+// Whole-row nucleus rows (top_k 0) whose top-p cut lies deeper than the 64
+// best logits that the fused pass keeps: finished by the row's finishing
+// workgroup of the fused kernel itself (all its waves), in the LDS of its
+// staging buffers, so no second launch is needed.
 //
 // It computes what fg_sampler_select (src/sampler.c:80-122) computes over the
 // whole row: sort by (value desc, id asc), cut at the first position where
 // the running untempered mass reaches top_p, then draw from the cut set with
 // the tempered weights.  Sorting 151,936 logits per row is not needed.  Both
 // steps are a weighted select: find the first element, in that order, at
-// which a running sum crosses a target.  One workgroup of 512 threads owns a
-// row and descends through histograms of mass in LDS:
-//   level 1  2048 bins of value, bin = floor((vmax - v) * 64) computed in
-//            exact f64, so equal values share a bin and bins follow the order;
+// which a running sum crosses a target.  One workgroup owns a row and
+// descends through histograms of mass in LDS (sizes from NucCfg; the fused
+// kernel's: 256 threads, 512 bins, 2,048 collected):
+//   level 1  kBins bins of value, bin = floor((vmax - v) * kBins / 32)
+//            computed in exact f64, so equal values share a bin and bins
+//            follow the order (32 logit units below the maximum and beyond
+//            share the last bin);
 //   level n  the chosen bin as a range of 63-bit value-order composites
-//            (value key << 31 | ~id, unique per element), split into 2048
+//            (value key << 31 | ~id, unique per element), split into kBins
 //            equal sub-ranges, until a range is small enough;
 //   collect  once the chosen bin holds at most kCollect elements they are
 //            gathered into LDS, sorted with a bitonic network and scanned in
@@ -25,29 +30,42 @@
 // an earlier bin than the cut.
 #pragma once
 
-#include "fg_sample_kernels.hpp"
+// Included by fg_sample_kernels.hpp, before the fused kernel (it uses the
+// sampler's types and helpers defined there).
 
 namespace fg {
 
-constexpr int kNucBlock = 512;
-constexpr int kNucWaves = kNucBlock / kWave;
-constexpr uint32_t kNucBins = 2048;
-constexpr uint32_t kBinsPer = kNucBins / kNucBlock;
-constexpr uint32_t kCollect = 4096;
-constexpr uint32_t kListPer = kCollect / kNucBlock;
+// Sizes of the descent: threads of the workgroup, bins per level, entries a
+// bin may hold to be collected and sorted.
+template <int kBlock_, uint32_t kBins_, uint32_t kCollect_, uint32_t kQuads_>
+struct NucCfg {
+  static constexpr uint32_t kQuads = kQuads_;  // 16-byte quads per thread per loop step
+  static constexpr int kBlock = kBlock_;
+  static constexpr int kWaves = kBlock_ / kWave;
+  static constexpr uint32_t kBins = kBins_;
+  static constexpr uint32_t kBinsPer = kBins_ / kBlock_;
+  static constexpr uint32_t kCollect = kCollect_;
+  static constexpr uint32_t kListPer = kCollect_ / kBlock_;
+  static constexpr double kValueBinScale = static_cast<double>(kBins_) / 32.0;
+};
+// The fused kernel's: four waves, in the LDS of the staging buffers, and
+// few enough registers per thread that the kernel keeps three workgroups
+// per CU with no stack.
+using FusedNuc = NucCfg<256, 512, 1024, 1>;
+
 constexpr uint32_t kMaxLevels = 8;
-constexpr double kValueBinScale = 64.0;
 constexpr uint32_t kNoBin = 0xffffffffu;
 
+template <class C>
 struct NucLds {
-  uint32_t cnt[kNucBins];
-  double mass[kNucBins];    // untempered exp(v - vmax)
-  double tmass[kNucBins];   // tempered exp((v - vmax) / T)
-  double tmass1[kNucBins];  // level-1 tempered mass, kept for the draw
-  uint32_t cnt1[kNucBins];  // level-1 counts, kept for the draw
-  uint64_t list[kCollect];
-  double wave_a[kNucWaves];
-  double wave_b[kNucWaves];
+  uint32_t cnt[C::kBins];
+  double mass[C::kBins];    // untempered exp(v - vmax)
+  double tmass[C::kBins];   // tempered exp((v - vmax) / T)
+  double tmass1[C::kBins];  // level-1 tempered mass, kept for the draw
+  uint32_t cnt1[C::kBins];  // level-1 counts, kept for the draw
+  uint64_t list[C::kCollect];
+  double wave_a[C::kWaves];
+  double wave_b[C::kWaves];
   uint64_t lo, hi;  // composite range (refinement)
   uint32_t pick;    // chosen bin / list index (atomicMin)
   uint32_t last;    // last non-empty bin + 1 (atomicMax)
@@ -79,9 +97,10 @@ struct Pick {
   double w_m, w_t;          // weight of comp itself
 };
 
+template <class C>
 __device__ __forceinline__ uint32_t value_bin(double vmax, float v) {
-  const double d = (vmax - static_cast<double>(v)) * kValueBinScale;
-  return d >= static_cast<double>(kNucBins - 1u) ? kNucBins - 1u : static_cast<uint32_t>(d);
+  const double d = (vmax - static_cast<double>(v)) * C::kValueBinScale;
+  return d >= static_cast<double>(C::kBins - 1u) ? C::kBins - 1u : static_cast<uint32_t>(d);
 }
 
 __device__ __forceinline__ float pen_value(const RowView& r, float v, uint32_t c) {
@@ -93,8 +112,9 @@ __device__ __forceinline__ float row_value(const RowView& r, uint32_t i) {
 }
 
 // Calls f(v, id) for every element of the row (penalised value), each once
-// across the workgroup.  Two 16-byte quads per thread are in flight.
-template <class Fn>
+// across the workgroup.  C::kQuads (1 or 2) 16-byte quads per thread are in
+// flight.
+template <class C, class Fn>
 __device__ __forceinline__ void for_each_element(const RowView& r, Fn&& f) {
   const uint32_t tid = threadIdx.x;
   uint32_t head = 0u;
@@ -102,9 +122,9 @@ __device__ __forceinline__ void for_each_element(const RowView& r, Fn&& f) {
     const uint32_t nq = r.vocab / 4u;
     const f4* lq = reinterpret_cast<const f4*>(r.lrow);
     const u4* cq = reinterpret_cast<const u4*>(r.crow);
-    for (uint32_t q = tid; q < nq; q += 2u * kNucBlock) {
-      const uint32_t q1 = q + kNucBlock;
-      const bool ok1 = q1 < nq;
+    for (uint32_t q = tid; q < nq; q += C::kQuads * C::kBlock) {
+      const uint32_t q1 = q + C::kBlock;
+      const bool ok1 = C::kQuads > 1u && q1 < nq;
       const uint32_t q1c = ok1 ? q1 : q;
       const f4 x0 = lq[q], x1 = lq[q1c];
       u4 y0 = {0u, 0u, 0u, 0u}, y1 = {0u, 0u, 0u, 0u};
@@ -121,12 +141,13 @@ __device__ __forceinline__ void for_each_element(const RowView& r, Fn&& f) {
     }
     head = nq * 4u;
   }
-  for (uint32_t i = head + tid; i < r.vocab; i += kNucBlock) f(row_value(r, i), i);
+  for (uint32_t i = head + tid; i < r.vocab; i += C::kBlock) f(row_value(r, i), i);
 }
 
 // Exclusive block scan of two f64 series (one value each per thread); also
 // returns the totals.  All threads must call it.
-__device__ inline void block_scan2(NucLds& s, double a, double b, double* ea, double* eb,
+template <class C>
+__device__ inline void block_scan2(NucLds<C>& s, double a, double b, double* ea, double* eb,
                                    double* ta, double* tb) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform
   const uint32_t lane = lane_id();
@@ -138,7 +159,7 @@ __device__ inline void block_scan2(NucLds& s, double a, double b, double* ea, do
   }
   __syncthreads();
   double oa = 0.0, ob = 0.0, sa = 0.0, sb = 0.0;
-  for (uint32_t w = 0; w < kNucWaves; w++) {
+  for (uint32_t w = 0; w < C::kWaves; w++) {
     const double xa = s.wave_a[w], xb = s.wave_b[w];
     if (w < wave) {
       oa += xa;
@@ -155,20 +176,21 @@ __device__ inline void block_scan2(NucLds& s, double a, double b, double* ea, do
 }
 
 // Fills cnt / mass / tmass for one level over the elements with c >= floor.
-__device__ inline void histogram_pass(NucLds& s, const RowView& r, const Level& lv,
+template <class C>
+__device__ inline void histogram_pass(NucLds<C>& s, const RowView& r, const Level& lv,
                                       uint64_t floor) {
-  for (uint32_t b = threadIdx.x; b < kNucBins; b += kNucBlock) {
+  for (uint32_t b = threadIdx.x; b < C::kBins; b += C::kBlock) {
     s.cnt[b] = 0u;
     s.mass[b] = 0.0;
     s.tmass[b] = 0.0;
   }
   __syncthreads();
-  for_each_element(r, [&](float v, uint32_t i) {
+  for_each_element<C>(r, [&](float v, uint32_t i) {
     const uint64_t c = value_comp(v, i);
     if (c == 0ull || c < floor) return;
     uint32_t b;
     if (lv.value) {
-      b = value_bin(r.vmax, v);
+      b = value_bin<C>(r.vmax, v);
     } else {
       if (c < lv.lo || c > lv.hi) return;
       b = static_cast<uint32_t>((lv.hi - c) >> lv.shift);
@@ -194,8 +216,10 @@ struct BinChoice {
   bool crossed;
 };
 
-__device__ inline BinChoice choose_bin(NucLds& s, double above, double target, bool tempered,
+template <class C>
+__device__ inline BinChoice choose_bin(NucLds<C>& s, double above, double target, bool tempered,
                                        bool inclusive, uint32_t limit) {
+  constexpr uint32_t kBinsPer = C::kBinsPer;
   const uint32_t tid = threadIdx.x;
   const bool saved = limit != kNoBin;
   const uint32_t bb = tid * kBinsPer;
@@ -217,7 +241,7 @@ __device__ inline BinChoice choose_bin(NucLds& s, double above, double target, b
     s.last = 0u;
   }
   double ex, ex_o, tot, tot_o;
-  block_scan2(s, sc, so, &ex, &ex_o, &tot, &tot_o);  // its barriers order the resets
+  block_scan2<C>(s, sc, so, &ex, &ex_o, &tot, &tot_o);  // its barriers order the resets
   {
     uint32_t last = 0u;
 #pragma unroll
@@ -264,17 +288,19 @@ __device__ inline BinChoice choose_bin(NucLds& s, double above, double target, b
 
 // Gathers the members of `bin` of level lv (c >= floor) into s.list, sorted
 // descending; returns their number (<= kCollect).
-__device__ inline uint32_t collect_sorted(NucLds& s, const RowView& r, const Level& lv,
+template <class C>
+__device__ inline uint32_t collect_sorted(NucLds<C>& s, const RowView& r, const Level& lv,
                                           uint32_t bin, uint64_t floor) {
+  constexpr uint32_t kCollect = C::kCollect;
   const uint32_t tid = threadIdx.x;
   if (tid == 0) s.n = 0u;
   __syncthreads();
-  for_each_element(r, [&](float v, uint32_t i) {
+  for_each_element<C>(r, [&](float v, uint32_t i) {
     const uint64_t c = value_comp(v, i);
     if (c == 0ull || c < floor) return;
     bool in;
     if (lv.value)
-      in = value_bin(r.vmax, v) == bin;
+      in = value_bin<C>(r.vmax, v) == bin;
     else
       in = c >= lv.lo && c <= lv.hi && static_cast<uint32_t>((lv.hi - c) >> lv.shift) == bin;
     if (in) {
@@ -286,11 +312,11 @@ __device__ inline uint32_t collect_sorted(NucLds& s, const RowView& r, const Lev
   const uint32_t n = min(s.n, kCollect);
   uint32_t P = 1u;
   while (P < n) P <<= 1;
-  for (uint32_t i = n + tid; i < P; i += kNucBlock) s.list[i] = 0ull;
+  for (uint32_t i = n + tid; i < P; i += C::kBlock) s.list[i] = 0ull;
   __syncthreads();
   for (uint32_t k = 2u; k <= P; k <<= 1) {
     for (uint32_t j = k >> 1; j > 0u; j >>= 1) {
-      for (uint32_t i = tid; i < P; i += kNucBlock) {
+      for (uint32_t i = tid; i < P; i += C::kBlock) {
         const uint32_t ixj = i ^ j;
         if (ixj > i) {
           const uint64_t x = s.list[i], y = s.list[ixj];
@@ -310,8 +336,10 @@ __device__ inline uint32_t collect_sorted(NucLds& s, const RowView& r, const Lev
 // Scans the first n (>= 1) entries of the sorted list in order (running
 // weights start at above_m / above_t) and returns the first crossing entry,
 // or the n-th if none crosses.
-__device__ inline Pick scan_list(NucLds& s, const RowView& r, uint32_t n, double above_m,
+template <class C>
+__device__ inline Pick scan_list(NucLds<C>& s, const RowView& r, uint32_t n, double above_m,
                                  double above_t, double target, bool tempered, bool inclusive) {
+  constexpr uint32_t kListPer = C::kListPer;
   const uint32_t tid = threadIdx.x;
   double wm[kListPer], wt[kListPer], sm = 0.0, st = 0.0;
 #pragma unroll
@@ -328,7 +356,7 @@ __device__ inline Pick scan_list(NucLds& s, const RowView& r, uint32_t n, double
   }
   if (tid == 0) s.pick = kNoBin;
   double exm, ext, totm, tott;
-  block_scan2(s, sm, st, &exm, &ext, &totm, &tott);
+  block_scan2<C>(s, sm, st, &exm, &ext, &totm, &tott);
   {
     double cm = above_m + exm, ct = above_t + ext;
 #pragma unroll
@@ -374,16 +402,17 @@ __device__ inline Pick scan_list(NucLds& s, const RowView& r, uint32_t n, double
 // it is small enough, else narrows the range and descends.  `above_*` are
 // the weights ranked before the bin.  *refined reports whether the result
 // came from a level below lv.
-__device__ inline Pick descend_from(NucLds& s, const RowView& r, Level lv, uint32_t bin,
+template <class C>
+__device__ inline Pick descend_from(NucLds<C>& s, const RowView& r, Level lv, uint32_t bin,
                                     uint32_t count, double above_m, double above_t,
                                     uint64_t floor, double target, bool tempered, bool inclusive,
                                     bool* refined) {
   *refined = false;
   for (uint32_t level = 0; level < kMaxLevels; level++) {
-    if (count <= kCollect) {
-      const uint32_t n = collect_sorted(s, r, lv, bin, floor);
+    if (count <= C::kCollect) {
+      const uint32_t n = collect_sorted<C>(s, r, lv, bin, floor);
       if (n == 0u) break;
-      return scan_list(s, r, n, above_m, above_t, target, tempered, inclusive);
+      return scan_list<C>(s, r, n, above_m, above_t, target, tempered, inclusive);
     }
     *refined = true;
     // The chosen bin becomes the next level's composite range.
@@ -394,9 +423,9 @@ __device__ inline Pick descend_from(NucLds& s, const RowView& r, Level lv, uint3
       }
       __syncthreads();
       uint64_t mn = ~0ull, mx = 0ull;
-      for_each_element(r, [&](float v, uint32_t i) {
+      for_each_element<C>(r, [&](float v, uint32_t i) {
         const uint64_t c = value_comp(v, i);
-        if (c == 0ull || c < floor || value_bin(r.vmax, v) != bin) return;
+        if (c == 0ull || c < floor || value_bin<C>(r.vmax, v) != bin) return;
         mn = c < mn ? c : mn;
         mx = c > mx ? c : mx;
       });
@@ -418,14 +447,14 @@ __device__ inline Pick descend_from(NucLds& s, const RowView& r, Level lv, uint3
       lv.lo = top - lv.lo > width ? top - width : lv.lo;
       lv.hi = top;
     }
-    // Each range level narrows the range by kNucBins, so 63-bit composites
-    // need at most 6 levels; kMaxLevels only bounds the loop.
+    // Each range level narrows the range by kBins (512: 9 bits), so 63-bit
+    // composites need at most 7 levels; kMaxLevels only bounds the loop.
     uint32_t sh = 0u;
-    while (((lv.hi - lv.lo) >> sh) >= kNucBins) sh++;
+    while (((lv.hi - lv.lo) >> sh) >= C::kBins) sh++;
     lv.shift = sh;
-    histogram_pass(s, r, lv, floor);
+    histogram_pass<C>(s, r, lv, floor);
     const BinChoice ch =
-        choose_bin(s, tempered ? above_t : above_m, target, tempered, inclusive, kNoBin);
+        choose_bin<C>(s, tempered ? above_t : above_m, target, tempered, inclusive, kNoBin);
     if (ch.bin == kNoBin) break;
     bin = ch.bin;
     count = ch.count;
@@ -435,40 +464,59 @@ __device__ inline Pick descend_from(NucLds& s, const RowView& r, Level lv, uint3
   return Pick{0ull, 0u, 0.0, 0.0, 0.0, 0.0};  // not reached for a consistent row
 }
 
-// Grid: one workgroup per row of the batch.  Rows that are not deep nucleus
-// rows of this launch return at once.
-__global__ void __launch_bounds__(kNucBlock) nucleus_rows_kernel(SampleArgs a) {
-  __shared__ NucLds s;
-  const uint32_t row = blockIdx.x;
+// What the descent needs of one deep row (by value: the sampler's argument
+// block is too large to pass to a function that is not inlined).
+struct DeepRow {
+  const float* lrow;
+  const uint32_t* crow;  // null: no penalties
+  RowParams p;
+  uint32_t vocab;
+  float u;               // the row's uniform
+  float vmax;            // the row's largest finite (penalised) value
+  uint32_t* token;
+  float* token_logit;    // optional
+  int32_t* status;       // optional
+};
+
+// The descent for one deep row; every thread of the workgroup calls it.
+// Writes the row's token, logit and status.  Inlined: a call would give the
+// whole kernel a stack (the callee-saved registers it uses).
+template <class C>
+__device__ __forceinline__ void nucleus_deep_row(
+    const float* lrow, const uint32_t* crow, float temperature, float top_p, float presence,
+    float frequency, float repetition, uint32_t vocab, float u_row, float vmax, uint32_t* token,
+    float* token_logit, int32_t* status, NucLds<C>& s) {
+  RowParams p{};
+  p.temperature = temperature;
+  p.top_p = top_p;
+  p.presence = presence;
+  p.frequency = frequency;
+  p.repetition = repetition;
+  const DeepRow dr{lrow, crow, p, vocab, u_row, vmax, token, token_logit, status};
   const uint32_t tid = threadIdx.x;
-  const RowParams p = row_controls(a, row);
-  if (!(p.temperature > 0.0f) || p.top_k != 0u || a.nuc_deep[row] == 0u) return;
-  const bool pen = (p.flags & kRowPenalties) && a.counts != nullptr;
-  const float* lrow = a.logits + static_cast<uint64_t>(row) * a.lstride;
-  const uint32_t* crow = pen ? a.counts + static_cast<uint64_t>(row) * a.cstride : nullptr;
-  const bool vec = (reinterpret_cast<uintptr_t>(lrow) & 15u) == 0u &&
-                   (!crow || (reinterpret_cast<uintptr_t>(crow) & 15u) == 0u);
-  const RowView r{lrow, crow, p, a.vocab, vec, static_cast<double>(a.nuc_max[row]),
+  const bool vec = (reinterpret_cast<uintptr_t>(dr.lrow) & 15u) == 0u &&
+                   (!dr.crow || (reinterpret_cast<uintptr_t>(dr.crow) & 15u) == 0u);
+  const RowView r{dr.lrow, dr.crow, p, dr.vocab, vec, static_cast<double>(dr.vmax),
                   1.0 / static_cast<double>(p.temperature)};
 
   // Level 1 over every finite element: both masses per value bin.
   const Level l1{true, 0ull, 0ull, 0u};
-  histogram_pass(s, r, l1, kFiniteComp);
-  for (uint32_t b = tid; b < kNucBins; b += kNucBlock) {
+  histogram_pass<C>(s, r, l1, kFiniteComp);
+  for (uint32_t b = tid; b < C::kBins; b += C::kBlock) {
     s.tmass1[b] = s.tmass[b];
     s.cnt1[b] = s.cnt[b];
   }
   double total_m, total_t;
   {
     double sm = 0.0, st = 0.0, e0, e1;
-    for (uint32_t b = tid; b < kNucBins; b += kNucBlock) {
+    for (uint32_t b = tid; b < C::kBins; b += C::kBlock) {
       sm += s.mass[b];
       st += s.tmass[b];
     }
-    block_scan2(s, sm, st, &e0, &e1, &total_m, &total_t);
+    block_scan2<C>(s, sm, st, &e0, &e1, &total_m, &total_t);
   }
 
-  float u = a.uniforms[row];
+  float u = dr.u;
   if (!is_finite_bits(__float_as_uint(u)) || u < 0.0f) u = 0.0f;
   if (u >= 1.0f) u = __uint_as_float(0x3f7fffffu);  // nextafterf(1, 0)
   bool refined;
@@ -477,49 +525,49 @@ __global__ void __launch_bounds__(kNucBlock) nucleus_rows_kernel(SampleArgs a) {
   if (p.top_p >= 1.0f) {
     // The cut keeps every finite logit: draw from the level-1 histogram.
     const double target = static_cast<double>(u) * total_t;
-    const BinChoice ch = choose_bin(s, 0.0, target, true, false, kNoBin);
+    const BinChoice ch = choose_bin<C>(s, 0.0, target, true, false, kNoBin);
     if (ch.bin != kNoBin)
-      d = descend_from(s, r, l1, ch.bin, ch.count, ch.before_o, ch.before_c, kFiniteComp, target,
+      d = descend_from<C>(s, r, l1, ch.bin, ch.count, ch.before_o, ch.before_c, kFiniteComp, target,
                        true, false, &refined);
   } else {
     // Cut: first position where the running mass reaches top_p of the total.
     const double target = static_cast<double>(p.top_p) * total_m;
-    const BinChoice ch = choose_bin(s, 0.0, target, false, true, kNoBin);
+    const BinChoice ch = choose_bin<C>(s, 0.0, target, false, true, kNoBin);
     Pick c{0ull, 0u, 0.0, 0.0, 0.0, 0.0};
     if (ch.bin != kNoBin)
-      c = descend_from(s, r, l1, ch.bin, ch.count, ch.before_c, ch.before_o, kFiniteComp, target,
+      c = descend_from<C>(s, r, l1, ch.bin, ch.count, ch.before_c, ch.before_o, kFiniteComp, target,
                        false, true, &refined);
     if (c.comp != 0ull) {
       const double draw = static_cast<double>(u) * (c.above_t + c.w_t);
       // Bins before the cut's bin lie wholly inside the cut set.
-      const BinChoice dh = choose_bin(s, 0.0, draw, true, false, ch.bin);
+      const BinChoice dh = choose_bin<C>(s, 0.0, draw, true, false, ch.bin);
       if (dh.crossed) {
-        d = descend_from(s, r, l1, dh.bin, dh.count, 0.0, dh.before_c, kFiniteComp, draw, true,
+        d = descend_from<C>(s, r, l1, dh.bin, dh.count, 0.0, dh.before_c, kFiniteComp, draw, true,
                          false, &refined);
       } else if (!refined) {
         // The cut's bin is still sorted in LDS: draw among its entries up
         // to the cut, after all the bins before it.
-        d = scan_list(s, r, c.idx + 1u, 0.0, dh.total_c, draw, true, false);
+        d = scan_list<C>(s, r, c.idx + 1u, 0.0, dh.total_c, draw, true, false);
       } else {
         // Rare: the cut needed a finer level; rerun the descent above it.
-        histogram_pass(s, r, l1, c.comp);
-        const BinChoice dd = choose_bin(s, 0.0, draw, true, false, kNoBin);
+        histogram_pass<C>(s, r, l1, c.comp);
+        const BinChoice dd = choose_bin<C>(s, 0.0, draw, true, false, kNoBin);
         if (dd.bin != kNoBin)
-          d = descend_from(s, r, l1, dd.bin, dd.count, dd.before_o, dd.before_c, c.comp, draw,
+          d = descend_from<C>(s, r, l1, dd.bin, dd.count, dd.before_o, dd.before_c, c.comp, draw,
                            true, false, &refined);
       }
     }
   }
   if (tid == 0) {
     if (d.comp == 0ull) {
-      a.tokens[row] = kInvalidId;
-      if (a.row_status) a.row_status[row] = kStLimit;
+      *dr.token = kInvalidId;
+      if (dr.status) *dr.status = kStLimit;
     } else {
       const uint32_t id = comp_id(d.comp);
-      a.tokens[row] = id;
+      *dr.token = id;
       // The logit keeps its sign of zero: read it back from the row.
-      if (a.token_logits) a.token_logits[row] = row_value(r, id);
-      if (a.row_status) a.row_status[row] = kStOk;
+      if (dr.token_logit) *dr.token_logit = row_value(r, id);
+      if (dr.status) *dr.status = kStOk;
     }
   }
 }

@@ -99,8 +99,6 @@ struct SampleArgs {
   double* zsum;          // [slot][3] whole-row nucleus mass (max, sum, error bound)
   uint32_t* row_done;    // [rows * kLineWords] arrivals, one cache line per row,
                          // reset by the last workgroup
-  uint32_t* nuc_deep;    // [rows] whole-row nucleus: 1 = cut deeper than the kMaxK best
-  float* nuc_max;        // [rows] whole-row nucleus: the row's largest finite value
   uint64_t* trace;       // FG_SAMPLE_TRACE builds only: [workgroup][16] timestamps
   // Controls carried by value (inline > 0): rows [0, inline) of the table,
   // read from here and written to `params` by workgroup 0 for later
@@ -498,7 +496,7 @@ __device__ __forceinline__ Mass wave_mass_combine(double m, double z, double e) 
 // end); gbest: the row's greedy composite; (m, z): the row's tempered
 // log-sum-exp pair for log-probs; zs: the row's untempered mass for a
 // whole-row nucleus.  Writes token, logit, status and log-probs.
-__device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint32_t row,
+__device__ inline int32_t finish_row(const SampleArgs& a, const RowParams& p, uint32_t row,
                                   uint64_t fin, uint64_t gbest, double m, double z, Mass zs,
                                   const float* lrow, const uint32_t* crow, bool pen, float u,
                                   double inv_t) {
@@ -636,15 +634,12 @@ __device__ inline void finish_row(const SampleArgs& a, const RowParams& p, uint3
       a.lp_ids[static_cast<uint64_t>(row) * L + lane] = id;
     }
   }
-  if (nuc && lane == 0) {
-    a.nuc_deep[row] = status == kStLimit ? 1u : 0u;
-    a.nuc_max[row] = key_to_float(comp_key(readlane64(fin, 0)));
-  }
   if (lane == 0) {
     a.tokens[row] = token;
     if (a.token_logits) a.token_logits[row] = token_logit;
     if (a.row_status) a.row_status[row] = status;
   }
+  return status;
 }
 
 // ---- streaming ---------------------------------------------------------------
@@ -1172,10 +1167,16 @@ __device__ __forceinline__ void rank_place_lists(const uint64_t* lists, uint32_t
   rank_place<8>(lists, 32u, pos < kk ? lists[c * 32u + pos] : 0ull, kk, out);
 }
 
+}  // namespace fg
+
+#include "fg_nucleus_kernels.hpp"
+
+namespace fg {
+
 // ---- the fused kernel ------------------------------------------------------
 
 template <class F>
-__global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
+__global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
   __shared__ uint64_t s_buf[F::kTop ? kWaves : 1][F::kTop ? kCap + kWave : 1];
   __shared__ uint64_t s_top[kWaves][kWave];
   __shared__ uint64_t s_greedy[kWaves];
@@ -1375,6 +1376,40 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
     rank_place<kWaves>(&s_top[0][0], kWave, mine, kk, s_rank);
     __syncthreads();
   }
+  // Launches with whole-row nucleus rows: a workgroup's waves stay to the
+  // end, where wave 0 tells them (through LDS, at one barrier every path of
+  // every wave reaches) whether its row's cut lies below the kMaxK best; if
+  // so all four run the deep-row descent, in the staging LDS.
+  __shared__ uint32_t s_nuc_deep;
+  __shared__ float s_nuc_vmax;
+  auto nuc_tail = [&](bool deep, float vmax) __attribute__((always_inline)) {
+    if (wave == 0 && lane == 0) {
+      s_nuc_deep = deep ? 1u : 0u;
+      s_nuc_vmax = vmax;
+    }
+    __syncthreads();
+    // (Nucleus rows keep top lists, so launches with them have kTop.)
+#ifndef FG_NO_DEEP_CALL
+    if constexpr (F::kTop) {
+#else
+    if constexpr (false) {
+#endif
+      if (__builtin_expect(s_nuc_deep != 0u, 0)) {
+        static_assert(sizeof(NucLds<FusedNuc>) <= sizeof(s_buf), "deep-row LDS");
+        // Everything the descent needs is re-read here, so the streaming
+        // code above carries none of it.
+        const RowParams q = row_controls(a, row);
+        const bool qpen = (q.flags & kRowPenalties) && a.counts != nullptr;
+        nucleus_deep_row<FusedNuc>(
+            a.logits + static_cast<uint64_t>(row) * a.lstride,
+            qpen ? a.counts + static_cast<uint64_t>(row) * a.cstride : nullptr, q.temperature,
+            q.top_p, q.presence, q.frequency, q.repetition, a.vocab, a.uniforms[row], s_nuc_vmax,
+            a.tokens + row, a.token_logits ? a.token_logits + row : nullptr,
+            a.row_status ? a.row_status + row : nullptr,
+            *reinterpret_cast<NucLds<FusedNuc>*>(&s_buf[0][0]));
+      }
+    }
+  };
   if (wave != 0) {
     if (F::kTop && fin_wg) {
       // The finisher's helpers: wave 0 fills the lists, all four rank them.
@@ -1382,6 +1417,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       rank_place_lists(&s_top[0][0], wave, kk, s_rank);
       __syncthreads();
     }
+    if constexpr (F::kNuc) nuc_tail(false, 0.0f);
     return;
   }
   uint64_t fin = 0ull;
@@ -1443,6 +1479,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
       FG_TRACE(a, 4);
       if (arrived != a.chunks - 1u) {
         FG_TRACE_FLUSH(a);
+        if constexpr (F::kNuc) nuc_tail(false, 0.0f);
         return;
       }
     }
@@ -1617,14 +1654,17 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(SampleArgs a) {
   // One copy of the check and of the finish serves both paths.
   if (spec) fin = spec_check(a, p, row, pen, lrow, crow, fin, kk, s_ks, ks0, s_buf[0], &s_wg_key);
   FG_TRACE(a, 6);
+  int32_t status = kStOk;
   if (gave_up)
     timeout_row(a, row);
   else
-    finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
+    status = finish_row(a, p, row, fin, g, m, z, zs, lrow, crow, pen, urow, inv_t);
   if (a.chunks != 1u && !fin_mode && !gfin_mode && lane == 0)
     store_coherent(&a.row_done[row * kLineWords], 0u);
   FG_TRACE(a, 7);
   FG_TRACE_FLUSH(a);
+  if constexpr (F::kNuc)
+    nuc_tail(nuc && status == kStLimit, key_to_float(comp_key(readlane64(fin, 0))));
 }
 
 }  // namespace fg

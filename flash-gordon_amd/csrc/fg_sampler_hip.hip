@@ -11,7 +11,6 @@
 #include "fg_sampler_hip.h"
 #include "fg_dense_kernels.hpp"
 #include "fg_lmhead_sample_kernels.hpp"
-#include "fg_nucleus_kernels.hpp"
 #include "fg_sample_kernels.hpp"
 #include "fg_split_kernels.hpp"
 #include "fg_unit_kernels.hpp"
@@ -19,8 +18,6 @@
 namespace {
 
 using fg::RowParams;
-
-__device__ uint32_t g_history_bad;  // set by history_count_kernel on an id >= vocab
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
@@ -276,8 +273,6 @@ struct Workspace {
   double* lse;              // [slots][2]
   double* zsum;             // [slots][3]
   uint32_t* row_done;       // [max_rows * kLineWords], zero between launches
-  uint32_t* nuc_deep;       // [max_rows]
-  float* nuc_max;           // [max_rows]
   uint64_t* trace;          // phase timestamps, FG_SAMPLE_TRACE builds only
   uint32_t* epoch;          // host: the last finisher launch's epoch (0: none yet)
   uint32_t cus;             // compute units of the device (co-residency check)
@@ -325,9 +320,7 @@ constexpr size_t kOffSpec = align256(kOffGreedy + sizeof(uint64_t) * kStaticSlot
 constexpr size_t kOffLse = align256(kOffSpec + sizeof(uint32_t) * kStaticSlots);
 constexpr size_t kOffZsum = align256(kOffLse + sizeof(double) * kStaticSlots * 2u);
 constexpr size_t kOffDone = align256(kOffZsum + sizeof(double) * kStaticSlots * 3u);
-constexpr size_t kOffDeep = align256(kOffDone + sizeof(uint32_t) * fg::kLineWords * kStaticMaxRows);
-constexpr size_t kOffNucMax = align256(kOffDeep + sizeof(uint32_t) * kStaticMaxRows);
-constexpr size_t kStaticBytes = align256(kOffNucMax + sizeof(float) * kStaticMaxRows);
+constexpr size_t kStaticBytes = align256(kOffDone + sizeof(uint32_t) * fg::kLineWords * kStaticMaxRows);
 static_assert(kStaticBytes == FG_SAMPLER_HIP_STATIC_BYTES, "header size out of date");
 
 static __device__ __align__(256) unsigned char scratch[kStaticBytes];
@@ -363,8 +356,6 @@ hipError_t static_workspace(Workspace* w) {
   w->lse = reinterpret_cast<double*>(p + kOffLse);
   w->zsum = reinterpret_cast<double*>(p + kOffZsum);
   w->row_done = reinterpret_cast<uint32_t*>(p + kOffDone);
-  w->nuc_deep = reinterpret_cast<uint32_t*>(p + kOffDeep);
-  w->nuc_max = reinterpret_cast<float*>(p + kOffNucMax);
   w->trace = nullptr;
   w->epoch = &g_static_epoch[dev];
   int cus = 0;
@@ -511,8 +502,6 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
   a.lse = w.lse;
   a.zsum = w.zsum;
   a.row_done = w.row_done;
-  a.nuc_deep = w.nuc_deep;
-  a.nuc_max = w.nuc_max;
   a.trace = w.trace;
   a.inline_rows = inline_rows;
   if (inline_rows) memcpy(a.row_inline, h_params, sizeof(RowParams) * inline_rows);
@@ -555,9 +544,6 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
     a.wait_ticks = ticks < UINT32_MAX ? static_cast<uint32_t>(ticks) : UINT32_MAX;
   }
   (vec ? kVecLaunch[bits] : kScalarLaunch)(grid, stream, a);
-  // Whole-row nucleus rows whose cut lies past the kMaxK best are finished
-  // by a second kernel; the others return at once.
-  if (any_nuc) fg::nucleus_rows_kernel<<<b->rows, fg::kNucBlock, 0, stream>>>(a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "sampler launch");
 }
@@ -885,38 +871,16 @@ fg_status fg_hip_history_build_wire(uint32_t* counts, uint64_t counts_stride, ui
 
 fg_status fg_hip_history_build(uint32_t* counts, uint64_t counts_stride, uint32_t vocab,
                                const uint32_t* ids, const uint64_t* offsets, uint32_t rows,
-                               void* stream, fg_error* err) {
-  if (!counts || !vocab || !offsets || !rows || counts_stride < vocab)
+                               int32_t* row_status, void* stream, fg_error* err) {
+  if (!counts || !vocab || !ids || !offsets || !rows || !row_status || counts_stride < vocab)
     return arg_fail(err, "invalid output history");
-  hipStream_t s = as_stream(stream);
-  const uint32_t zero = 0u;
-  hipError_t e = hipMemcpyToSymbolAsync(HIP_SYMBOL(g_history_bad), &zero, sizeof zero, 0,
-                                        hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) return hip_fail(err, e, "history flag reset");
-  const uint64_t total = static_cast<uint64_t>(rows) * vocab;
-  uint64_t blocks = (total + 255u) / 256u;
-  if (blocks > 65535u * 16u) blocks = 65535u * 16u;
-  fg::fill_u32_kernel<<<static_cast<uint32_t>(blocks), 256, 0, s>>>(counts, counts_stride, vocab,
-                                                                     rows, 0u);
-  uint32_t* bad = nullptr;
-  e = hipGetSymbolAddress(reinterpret_cast<void**>(&bad), HIP_SYMBOL(g_history_bad));
-  if (e != hipSuccess) return hip_fail(err, e, "history flag address");
-  if (ids) {
-    dim3 grid(8, rows);
-    fg::history_count_kernel<<<grid, 256, 0, s>>>(counts, counts_stride, vocab, ids, offsets, bad);
-  }
-  e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(err, e, "history launch");
-  uint32_t flag = 0u;
-  e = hipMemcpyFromSymbolAsync(&flag, HIP_SYMBOL(g_history_bad), sizeof flag, 0,
-                               hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return hip_fail(err, e, "history check");
-  if (flag) {
-    fg_error_set(err, FG_ERR_FORMAT, "history token is outside vocabulary");
-    return FG_ERR_FORMAT;
-  }
-  return FG_OK;
+  const uint32_t chunks = (vocab + fg::kWireRegion - 1u) / fg::kWireRegion;
+  if (static_cast<uint64_t>(rows) * chunks > 0x7fffffffull)
+    return arg_fail(err, "invalid output history");
+  fg::history_ids_build_kernel<<<rows * chunks, fg::kWireBlock, 0, as_stream(stream)>>>(
+      counts, counts_stride, vocab, ids, offsets, row_status, chunks);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "history launch");
 }
 
 fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t max_rows,
@@ -962,8 +926,6 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   const size_t done_bytes = sizeof(uint32_t) * fg::kLineWords * max_rows;
   if (e == hipSuccess) e = hipMalloc(&s->ws.row_done, done_bytes);
   if (e == hipSuccess) e = hipMemset(s->ws.row_done, 0, done_bytes);
-  if (e == hipSuccess) e = hipMalloc(&s->ws.nuc_deep, sizeof(uint32_t) * max_rows);
-  if (e == hipSuccess) e = hipMalloc(&s->ws.nuc_max, sizeof(float) * max_rows);
   if (e == hipSuccess) e = hipMemset(s->ws.params, 0, sizeof(RowParams) * max_rows);
 #ifdef FG_SAMPLE_TRACE
   if (e == hipSuccess) e = hipMalloc(&s->ws.trace, sizeof(uint64_t) * 16u * (groups_cap + max_rows));
@@ -991,8 +953,6 @@ void fg_sampler_hip_destroy(fg_sampler_hip* s) {
   (void)hipFree(s->ws.lse);
   (void)hipFree(s->ws.zsum);
   (void)hipFree(s->ws.row_done);
-  (void)hipFree(s->ws.nuc_deep);
-  (void)hipFree(s->ws.nuc_max);
   (void)hipFree(s->ws.trace);
   free(s->h_params);
   free(s);

@@ -140,46 +140,12 @@ __global__ __launch_bounds__(256) void topk_select_kernel(float* out_scores, uin
   }
 }
 
-__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* dst, uint64_t stride, uint32_t width,
-                                                     uint32_t rows, uint32_t value) {
-  const uint64_t total = static_cast<uint64_t>(rows) * width;
-  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint64_t r = i / width;
-    dst[r * stride + (i - r * width)] = value;
-  }
-}
-
 __device__ __forceinline__ void saturating_increment(uint32_t* p) {
   uint32_t old = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   while (old != 0xffffffffu) {
     const uint32_t seen = atomicCAS(p, old, old + 1u);
     if (seen == old) break;
     old = seen;
-  }
-}
-
-// src/output.c:601-617 for many rows: counts were cleared by fill_u32_kernel.
-// Grid: (blocks per row, rows).  An id >= vocab sets *bad.
-__global__ __launch_bounds__(256) void history_count_kernel(uint32_t* counts, uint64_t stride,
-                                                          uint32_t vocab, const uint32_t* ids,
-                                                          const uint64_t* offsets, uint32_t* bad) {
-  const uint32_t r = blockIdx.y;
-  const uint64_t b = offsets[r], e = offsets[r + 1];
-  for (uint64_t i = b + static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < e;
-       i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
-    const uint32_t id = ids[i];
-    if (id >= vocab) {
-      atomicOr(bad, 1u);
-      continue;
-    }
-    // A cleared row with fewer than UINT32_MAX ids cannot saturate: a plain
-    // atomic add avoids compare-and-swap retries on repeated ids.
-    uint32_t* c = counts + static_cast<uint64_t>(r) * stride + id;
-    if (e - b < 0xffffffffull)
-      atomicAdd(c, 1u);
-    else
-      saturating_increment(c);
   }
 }
 
@@ -286,6 +252,61 @@ __global__ __launch_bounds__(kWireBlock) void history_wire_build_kernel(
   uint32_t* crow = counts + static_cast<uint64_t>(r) * stride;
   if ((reinterpret_cast<uintptr_t>(crow + begin) & 15u) == 0u) {
     // 16-byte stores over the region's whole quads, then the tail.
+    const uint32_t quads = (end - begin) / 4u;
+    for (uint32_t q = tid; q < quads; q += kWireBlock)
+      reinterpret_cast<u4*>(crow + begin)[q] = reinterpret_cast<const u4*>(s_cnt)[q];
+    for (uint32_t i = begin + 4u * quads + tid; i < end; i += kWireBlock) crow[i] = s_cnt[i - begin];
+  } else {
+    for (uint32_t i = begin + tid; i < end; i += kWireBlock) crow[i] = s_cnt[i - begin];
+  }
+}
+
+// src/output.c:601-617 (fg_output_history_reset) per row, from plain id
+// lists, in one launch shaped like the wire builder: workgroup b owns region
+// b % chunks (kWireRegion counts) of row b / chunks.  It reads the row's ids
+// twice: first for the position of the first id outside the vocabulary (the
+// reference stops there), then counting in LDS the ids before it that fall
+// in its region.  The region is then written whole: cleared and counted in
+// one store per entry, no clearing pass and no global atomics.  A row of
+// more than kWireMaxCount ids is refused (FG_ERR_ARGUMENT, counts left as
+// they were); a row with an id outside the vocabulary gets FG_ERR_FORMAT and
+// the counts of the ids before it, as the reference leaves its table.  The
+// first workgroup of a row writes the row's status.
+__global__ __launch_bounds__(kWireBlock) void history_ids_build_kernel(
+    uint32_t* counts, uint64_t stride, uint32_t vocab, const uint32_t* ids,
+    const uint64_t* offsets, int32_t* row_status, uint32_t chunks) {
+  __shared__ __align__(16) uint32_t s_cnt[kWireRegion];
+  __shared__ uint32_t s_first_bad;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t r = blockIdx.x / chunks;
+  const uint32_t chunk = blockIdx.x - r * chunks;
+  const uint64_t b = offsets[r], n64 = offsets[r + 1] - b;
+  if (n64 > kWireMaxCount) {
+    if (chunk == 0 && tid == 0) row_status[r] = 2;  // FG_ERR_ARGUMENT
+    return;
+  }
+  const uint32_t n = static_cast<uint32_t>(n64);
+  const uint32_t* row_ids = ids + b;
+  const uint32_t begin = chunk * kWireRegion;
+  const uint32_t end = vocab - begin < kWireRegion ? vocab : begin + kWireRegion;
+  for (uint32_t i = tid; i < kWireRegion / 4u; i += kWireBlock)
+    reinterpret_cast<u4*>(s_cnt)[i] = u4{0u, 0u, 0u, 0u};
+  if (tid == 0) s_first_bad = n;
+  __syncthreads();
+  uint32_t first_bad = n;
+  for (uint32_t i = tid; i < n; i += kWireBlock)
+    if (row_ids[i] >= vocab && i < first_bad) first_bad = i;
+  if (first_bad < n) atomicMin(&s_first_bad, first_bad);
+  __syncthreads();
+  const uint32_t stop = s_first_bad;
+  for (uint32_t i = tid; i < stop; i += kWireBlock) {
+    const uint32_t id = row_ids[i];
+    if (id >= begin && id < end) atomicAdd(&s_cnt[id - begin], 1u);
+  }
+  if (chunk == 0 && tid == 0) row_status[r] = stop < n ? 4 : 0;  // FG_ERR_FORMAT / FG_OK
+  __syncthreads();
+  uint32_t* crow = counts + static_cast<uint64_t>(r) * stride;
+  if ((reinterpret_cast<uintptr_t>(crow + begin) & 15u) == 0u) {
     const uint32_t quads = (end - begin) / 4u;
     for (uint32_t q = tid; q < quads; q += kWireBlock)
       reinterpret_cast<u4*>(crow + begin)[q] = reinterpret_cast<const u4*>(s_cnt)[q];

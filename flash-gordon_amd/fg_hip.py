@@ -145,7 +145,7 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_hip_argmax_reduce": (C.c_int, [P, P, P, P, u32, C.POINTER(u32), P, E]),
         "fg_hip_topk_select": (C.c_int, [P, P, P, P, u32, u32, C.POINTER(u32), P, E]),
         "fg_hip_topk_reduce": (C.c_int, [P, P, P, P, u32, C.POINTER(u32), P, E]),
-        "fg_hip_history_build": (C.c_int, [P, u64, u32, P, P, u32, P, E]),
+        "fg_hip_history_build": (C.c_int, [P, u64, u32, P, P, u32, P, P, E]),
         "fg_hip_history_build_wire": (C.c_int, [P, u64, u32, P, P, u32, P, P, P, E]),
         "fg_output_history_encode": (C.c_int, [P, u32, C.POINTER(u32), C.POINTER(OutputHistory), E]),
         "fg_output_history_encode_vocab":
@@ -280,11 +280,12 @@ def _check_u64_offsets(offsets, rows):
         raise ValueError("offsets must hold rows + 1 64-bit entries")
 
 
-def history_build(counts, stride, vocab, ids, offsets, rows, stream=None):
+def history_build(counts, stride, vocab, ids, offsets, rows, row_status, stream=None):
+    """fg_hip_history_build: count tables from id lists; per-row status on the device."""
     _check_u64_offsets(offsets, rows)
     err = FgError()
     _check(lib().fg_hip_history_build(_ptr(counts), stride, vocab, _ptr(ids), _ptr(offsets),
-                                      rows, _stream(stream), C.byref(err)), err)
+                                      rows, _ptr(row_status), _stream(stream), C.byref(err)), err)
 
 
 def history_build_wire(counts, stride, vocab, payloads, offsets, rows, row_status,

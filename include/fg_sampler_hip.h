@@ -89,15 +89,21 @@ fg_status fg_hip_topk_reduce(float *output_scores, uint32_t *output_ids,
                              uint32_t count, uint32_t *output_count, void *stream,
                              fg_error *err);
 
-/* Dense history count tables from token lists: for each row r, counts[r*stride
- * .. +vocab) is cleared and then incremented once per id in
- * ids[offsets[r] .. offsets[r+1]), saturating at UINT32_MAX.  Replaces
- * fg_output_history_reset (src/output.c:601-617) for many rows at once.
- * An id >= vocab makes the call fail with FG_ERR_FORMAT after a device check
- * (this entry point synchronises `stream` to report it). */
+/* Dense history count tables from token lists, one launch, stream-ordered,
+ * no synchronisation: for each row r, counts[r*stride .. +vocab) is cleared
+ * and then incremented once per id in ids[offsets[r] .. offsets[r+1])
+ * (device memory).  Replaces fg_output_history_reset (src/output.c:601-617)
+ * for many rows at once, with its per-row outcome in row_status[r] (device
+ * int32): FG_OK; FG_ERR_FORMAT when an id is outside the vocabulary (the
+ * reference's "history token %u is outside vocabulary": the row holds the
+ * counts of the ids before it, as the reference's table does); or
+ * FG_ERR_ARGUMENT for more than FG_NATIVE_CONTEXT (262,144) ids (counts left
+ * as they were).  Calls on different streams touch only their own buffers.
+ * Errors: null pointers, rows == 0, stride < vocab. */
 fg_status fg_hip_history_build(uint32_t *counts, uint64_t counts_stride, uint32_t vocab,
                                const uint32_t *ids, const uint64_t *offsets,
-                               uint32_t rows, void *stream, fg_error *err);
+                               uint32_t rows, int32_t *row_status, void *stream,
+                               fg_error *err);
 
 /* The same count tables straight from FG_MSG_OUTPUT_HISTORY payloads
  * (fg_history.h): row r's payload is payloads[offsets[r] .. offsets[r+1])
@@ -214,7 +220,7 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip *sampler, const fg_sampler_hip_ba
  * one GPU shares that GPU's array: calls that overlap on one GPU (different
  * streams, or another thread) race and must be serialised by the caller. */
 #define FG_SAMPLER_HIP_STATIC_MAX_ROWS 256u
-#define FG_SAMPLER_HIP_STATIC_BYTES 2930688u
+#define FG_SAMPLER_HIP_STATIC_BYTES 2928640u
 fg_status fg_sampler_hip_sample_static(uint32_t vocab, const fg_sampler_config *configs,
                                        uint32_t flags, const fg_sampler_hip_batch *batch,
                                        void *stream, fg_error *err);

@@ -45,7 +45,7 @@ def test_argument_errors_without_device_work():
     err = fg_hip.FgError()
     assert lib.fg_sampler_hip_sample(None, None, None, C.byref(err)) == 2
     assert lib.fg_sampler_hip_set_configs(None, None, 0, 0, None, C.byref(err)) == 2
-    assert lib.fg_hip_history_build(None, 0, 0, None, None, 0, None, C.byref(err)) == 2
+    assert lib.fg_hip_history_build(None, 0, 0, None, None, 0, None, None, C.byref(err)) == 2
     lib.fg_sampler_hip_destroy(None)
 
 
@@ -64,6 +64,6 @@ def test_history_offsets_must_be_64_bit():
     with pytest.raises(ValueError):
         fg_hip.history_build_wire(None, 8, 8, None, off32, 4, None)
     with pytest.raises(ValueError):
-        fg_hip.history_build(None, 8, 8, None, off32, 4)
+        fg_hip.history_build(None, 8, 8, None, off32, 4, None)
     with pytest.raises(ValueError):
-        fg_hip.history_build(None, 8, 8, None, torch.zeros(4, dtype=torch.int64), 4)
+        fg_hip.history_build(None, 8, 8, None, torch.zeros(4, dtype=torch.int64), 4, None)

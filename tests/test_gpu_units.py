@@ -175,21 +175,66 @@ def test_topk_step_and_ladder_match_oracle(dev, k):
 
 
 def test_history_build_matches_oracle(dev):
+    """fg_hip_history_build: Zipf histories with repeats against the oracle's
+    tables (one launch, status per row on the device).  A row with an id
+    outside the vocabulary reports FG_ERR_FORMAT and holds the counts of the
+    ids before it (src/output.c:609-614 stops there); the other rows are
+    unaffected.  The columns past vocab are never written."""
     import torch
     rows, vocab = 6, 151_936
     ids = O.gen_zipf_ids(rows, 1024, vocab, 1.1, 7, 7)
     want = O.build_counts(ids, vocab)
     d = torch.full((rows, vocab + 8), 123, dtype=torch.int32, device=dev)
+    st = torch.full((rows,), -1, dtype=torch.int32, device=dev)
     offsets = torch.arange(0, (rows + 1) * 1024, 1024, dtype=torch.int64, device=dev)
-    fg_hip.history_build(d, vocab + 8, vocab, dev_u32(ids.reshape(-1), dev), offsets, rows)
+    fg_hip.history_build(d, vocab + 8, vocab, dev_u32(ids.reshape(-1), dev), offsets, rows, st)
+    torch.cuda.synchronize()
     got = u32(d)
     assert np.array_equal(got[:, :vocab], want)
     assert (got[:, vocab:] == 123).all()
-    bad = ids.reshape(-1).copy()
-    bad[100] = vocab
-    with pytest.raises(fg_hip.FgStatusError) as e:
-        fg_hip.history_build(d, vocab + 8, vocab, dev_u32(bad, dev), offsets, rows)
-    assert e.value.code == fg_hip.FG_ERR_FORMAT
+    assert (st.cpu().numpy() == 0).all()
+    bad = ids.copy()
+    bad[2, 100] = vocab
+    bad[2, 700] = vocab + 5
+    bad[4, 0] = 0xFFFFFFFF
+    fg_hip.history_build(d, vocab + 8, vocab, dev_u32(bad.reshape(-1), dev), offsets, rows, st)
+    torch.cuda.synchronize()
+    got = u32(d)
+    assert st.cpu().numpy().tolist() == [0, 0, fg_hip.FG_ERR_FORMAT, 0, fg_hip.FG_ERR_FORMAT, 0]
+    want_bad = want.copy()
+    want_bad[2] = O.build_counts(ids[2:3, :100], vocab)[0]
+    want_bad[4] = 0
+    assert np.array_equal(got[:, :vocab], want_bad)
+
+
+def test_history_build_on_two_streams(dev):
+    """Two builds on two streams at once (different tables, statuses and id
+    lists, one with a bad id): each reports only its own rows (no shared
+    flag), and neither waits for the device."""
+    import torch
+    rows, vocab = 4, 151_936
+    ids_a = O.gen_zipf_ids(rows, 2048, vocab, 1.1, 3, 3)
+    ids_b = O.gen_zipf_ids(rows, 512, vocab, 1.1, 5, 5)
+    ids_b[1, 17] = vocab
+    outs = []
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for ids, n, s in ((ids_a, 2048, streams[0]), (ids_b, 512, streams[1])):
+        d = torch.zeros((rows, vocab), dtype=torch.int32, device=dev)
+        st = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+        off = torch.arange(0, (rows + 1) * n, n, dtype=torch.int64, device=dev)
+        dids = dev_u32(ids.reshape(-1), dev)
+        torch.cuda.synchronize()
+        fg_hip.history_build(d, vocab, vocab, dids, off, rows, st, stream=s.cuda_stream)
+        outs.append((d, st, ids, dids, off))
+    torch.cuda.synchronize()
+    (da, sa, _, _, _), (db, sb, _, _, _) = outs
+    assert (sa.cpu().numpy() == 0).all()
+    assert sb.cpu().numpy().tolist() == [0, fg_hip.FG_ERR_FORMAT, 0, 0]
+    assert np.array_equal(u32(da), O.build_counts(ids_a, vocab))
+    want_b = O.build_counts(ids_b, vocab)
+    want_b[1] = O.build_counts(ids_b[1:2, :17], vocab)[0]
+    assert np.array_equal(u32(db), want_b)
 
 
 @pytest.mark.parametrize("pad,extra", [(1, 5), (0, 8)])
