@@ -466,6 +466,16 @@ __device__ __forceinline__ uint32_t wave_prefix_sum_u32(uint32_t x) {
   return x + (row < 2u ? (row == 0u ? 0u : r0) : (row == 2u ? r0 + r1 : r0 + r1 + r2));
 }
 
+// The wave's total in every lane.
+__device__ __forceinline__ uint32_t wave_reduce_sum_u32(uint32_t x) {
+  x += lane_xor<1>(x);
+  x += lane_xor<2>(x);
+  x += lane_xor<4>(x);
+  x += lane_xor<8>(x);
+  x += lane_xor<16>(x);
+  return x + lane_xor<32>(x);
+}
+
 // Inclusive sum over lanes >= this lane (used by the LDS radix select).
 __device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t v) {
   const uint32_t lane = lane_id();

@@ -621,6 +621,52 @@ fg_status fg_hip_topk_reduce(float* output_scores, uint32_t* output_ids,
   return FG_OK;
 }
 
+uint64_t fg_hip_topk_reduce_all_workspace_bytes(uint32_t count) {
+  return fg::reduce_all_bytes((static_cast<uint64_t>(count) + fg::kReduceTile - 1u) / fg::kReduceTile);
+}
+
+fg_status fg_hip_topk_reduce_all(float* output_scores, uint32_t* output_ids,
+                                 const float* input_scores, const uint32_t* input_ids,
+                                 uint32_t count, void* workspace, uint32_t* output_count,
+                                 void* stream, fg_error* err) {
+  if (!output_scores || !output_ids || !input_scores || !count || !workspace || !output_count ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255u))
+    return arg_fail(err, "invalid top-k reduction dispatch");
+  const uint32_t tiles = (count + fg::kReduceTile - 1u) / fg::kReduceTile;
+  // The grid-wide barriers need every tile's workgroup resident at once.
+  static std::atomic<int> occ{0};
+  int per_cu = occ.load(std::memory_order_relaxed);
+  if (!per_cu) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&fg::topk_reduce_all_kernel), fg::kReduceBlock,
+            0) != hipSuccess || per_cu < 0)
+      per_cu = 0;
+    occ.store(per_cu, std::memory_order_relaxed);
+  }
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return hip_fail(err, e, "top-k reduction device");
+  if (tiles > fg::kReduceAllMaxTiles ||
+      static_cast<uint64_t>(tiles) > static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(cus)) {
+    fg_error_set(err, FG_ERR_LIMIT, "%u tiles exceed the workgroups the device holds at once",
+                 tiles);
+    return FG_ERR_LIMIT;
+  }
+  const uint32_t out_n = count < fg::kReduceKeep ? count : fg::kReduceKeep;
+  // Tiles on the two XCDs that start first, when the padded grid still fits.
+  const uint64_t packed_grid = (static_cast<uint64_t>(tiles) + 1u) / 2u * 8u;
+  const bool packed = packed_grid <= static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(cus);
+  const uint32_t grid = packed ? static_cast<uint32_t>(packed_grid) : tiles;
+  fg::topk_reduce_all_kernel<<<grid, fg::kReduceBlock, 0, as_stream(stream)>>>(
+      output_scores, output_ids, input_scores, input_ids, count, out_n,
+      static_cast<uint8_t*>(workspace), tiles, packed ? 1u : 0u);
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(err, e, "top-k reduction launch");
+  *output_count = out_n;
+  return FG_OK;
+}
+
 struct fg_hip_output_slice {
   uint32_t vocab, ways, first_row, rows, max_batch;
   unsigned long long* d_keys;  // per batch row; zero between calls

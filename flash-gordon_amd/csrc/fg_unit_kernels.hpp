@@ -362,12 +362,22 @@ constexpr uint32_t kReduceNoBucket = 0xffu;
 __device__ uint64_t g_reduce_trace[512 * 32];
 #define FG_RDT(slot)                                                                    \
   do {                                                                                  \
+    __builtin_amdgcn_s_waitcnt(0);                                                      \
     if (threadIdx.x == 0 && blockIdx.x < 512u)                                        \
       g_reduce_trace[blockIdx.x * 32u + (slot)] = __builtin_amdgcn_s_memrealtime();     \
+  } while (0)
+#define FG_RDTR(row, slot)                                                              \
+  do {                                                                                  \
+    __builtin_amdgcn_s_waitcnt(0);                                                      \
+    if (threadIdx.x == 0 && (row) < 512u)                                               \
+      g_reduce_trace[(row) * 32u + (slot)] = __builtin_amdgcn_s_memrealtime();          \
   } while (0)
 #else
 #define FG_RDT(slot) \
   do {               \
+  } while (0)
+#define FG_RDTR(row, slot) \
+  do {                     \
   } while (0)
 #endif
 
@@ -806,6 +816,544 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_kernel(
       out_ids[o] = kInvalidId;
     }
   }
+}
+
+// ---- the whole top-512 scan in one launch --------------------------------------
+// One workgroup per 4096-entry tile, all resident at once.  Composites are
+// the 64-bit keys of fg_hip_topk_reduce's comparator (larger = earlier).
+//  1. Each tile finds its K-th largest composite v_t by radix steps over
+//     its composites in LDS (12 bits a step from the top, until the boundary
+//     bucket holds at most 64 entries, which one wave then ranks), with
+//     K = min(512, s + ceil(3 sqrt(s)) + 8) for the even share s =
+//     ceil(512 / tiles) (every entry of a smaller tile, and of a single
+//     tile), and publishes its entries at or above v_t and v_t itself; once
+//     they have landed it stores its slot: this call's tag with their number.
+//  2. Every workgroup waits for every slot to carry the tag, then gathers
+//     the published entries at or above V = max v_t into LDS, in the same
+//     order in every workgroup.  If there are at least 512, they hold the
+//     global top 512: an entry above the 512th is above V, so its tile
+//     published it.  Every workgroup then ranks its share of them against
+//     all of them (ties by position) and writes those of rank < 512 to
+//     their places.
+// Otherwise (the top entries crowded into few tiles: sorted or skewed
+// scores) every workgroup, deciding alike from the same data, takes a second
+// route: a radix select over the whole input with a global digit histogram
+// per round and a grid barrier after each, stopped once the entries at or
+// above the boundary bucket fit in LDS (or the key is complete: then the
+// boundary is one composite, repeated only by duplicate ids, and just the
+// copies still needed are taken), and a global list of those entries,
+// ranked the same way.
+// The output is the comparator order of fg_hip_topk_reduce, so it is what
+// iterating that kernel down to one tile leaves.
+constexpr uint32_t kReduceAllDigit = 12u;
+constexpr uint32_t kReduceAllBuckets = 1u << kReduceAllDigit;
+constexpr uint32_t kReduceAllRounds = 6u;       // 12 x 5 + 4 bits
+constexpr uint32_t kReduceAllList = 6144u;      // entries ranked in LDS
+constexpr uint32_t kReduceAllRegion = 1024u;    // entries one tile's region holds
+constexpr uint32_t kReduceAllSlack = 8u;        // K beyond a tile's share and its spread
+constexpr uint32_t kReduceAllMaxTiles = 1024u;  // tiles the gather's offsets hold
+struct ReduceAllWork {
+  uint32_t count;   // arrivals at the second route's grid barrier (back to 0 every use)
+  uint32_t gen;     // that barrier's uses so far (wraps)
+  uint32_t listed;  // second-route list entries
+  uint32_t ties;    // copies of an exact boundary composite taken
+  uint32_t call;    // calls so far (wraps): the slots' tag is call + 1
+};
+constexpr uint32_t kReduceAllHeader = 64u;
+constexpr uint64_t kReduceAllHistOffset = kReduceAllHeader;
+constexpr uint64_t kReduceAllListOffset =
+    kReduceAllHistOffset + uint64_t{kReduceAllRounds} * kReduceAllBuckets * sizeof(uint32_t);
+constexpr uint64_t kReduceAllSlotOffset =
+    kReduceAllListOffset + uint64_t{kReduceAllList} * (sizeof(uint64_t) + sizeof(uint32_t));
+static_assert(sizeof(ReduceAllWork) <= kReduceAllHeader, "header");
+static_assert(kReduceAllSlotOffset % 8u == 0u, "slot alignment");
+// Bytes of the workspace for `tiles` tiles: the fixed part, then per tile a
+// bound (8 B), a slot (8 B: tag << 32 | count) and a region of composites
+// and score bits.
+__host__ __device__ constexpr uint64_t reduce_all_bytes(uint64_t tiles) {
+  return kReduceAllSlotOffset + tiles * 2u * sizeof(uint64_t) +
+         tiles * kReduceAllRegion * (sizeof(uint64_t) + sizeof(uint32_t));
+}
+
+// Sense-reversing grid barrier: the last workgroup in (its arrival number
+// modulo `groups` is groups - 1) takes `groups` back off the count and
+// advances the generation; the others wait for the generation to move past
+// `gen`, which each workgroup read before its first arrival and counts along.
+// A fast workgroup's next arrival may land before the last one's subtraction:
+// arrival numbers are taken modulo `groups`, so it still counts right.
+__device__ __forceinline__ void grid_sync(ReduceAllWork* w, uint32_t groups, uint32_t& gen) {
+  wait_memory();  // this workgroup's published data first (see wait_memory)
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t o = atomicAdd(&w->count, 1u);
+    if (o % groups == groups - 1u) {
+      atomicSub(&w->count, groups);
+      __hip_atomic_store(&w->gen, gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      while (__hip_atomic_load(&w->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen)
+        __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  gen++;
+  __syncthreads();
+}
+
+// Workgroup barrier for LDS only: global loads already issued stay in flight
+// (__syncthreads also waits for them).
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt left alone
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ uint32_t load_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_agent64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The bucket, counting 4096 buckets from the top (count(b) for bucket b),
+// where the running count first reaches `need` (>= 1, at most the total):
+// s_sel = {bucket, count above it, its count}.  All kReduceBlock threads.
+template <class Count>
+__device__ __forceinline__ void top_bucket(Count count, uint32_t need, uint32_t* s_wave,
+                                           uint32_t* s_sel) {
+  constexpr uint32_t kScan = kReduceAllBuckets / kReduceBlock;
+  const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1u), wave = tid / kWave;
+  uint32_t c[kScan], sum = 0u;
+#pragma unroll
+  for (uint32_t j = 0; j < kScan; j++) {  // thread t: buckets 4095 - 8t down to 4088 - 8t
+    c[j] = count(kReduceAllBuckets - 1u - (tid * kScan + j));
+    sum += c[j];
+  }
+  const uint32_t incl = wave_prefix_sum_u32(sum);
+  if (lane == kWave - 1u) s_wave[wave] = incl;
+  __syncthreads();
+  uint32_t start = incl - sum;
+#pragma unroll
+  for (uint32_t w = 0; w < kReduceBlock / kWave; w++) start += w < wave ? s_wave[w] : 0u;
+#pragma unroll
+  for (uint32_t j = 0; j < kScan; j++) {
+    if (start < need && start + c[j] >= need) {
+      s_sel[0] = kReduceAllBuckets - 1u - (tid * kScan + j);
+      s_sel[1] = start;
+      s_sel[2] = c[j];
+    }
+    start += c[j];
+  }
+  __syncthreads();
+}
+
+// LDS histogram of the next digit of the composites under `prefix`.
+template <uint32_t kPer>
+__device__ __forceinline__ void digit_hist(uint32_t* lh, const uint64_t (&key)[kPer],
+                                           uint64_t prefix, uint32_t fixed, uint32_t width) {
+  const uint32_t shift = 64u - fixed - width;
+  const uint64_t hi_mask = fixed ? ~0ull << (64u - fixed) : 0ull;
+#pragma unroll
+  for (uint32_t j = 0; j < kReduceAllBuckets / kReduceBlock; j++) lh[j * kReduceBlock + threadIdx.x] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (uint32_t e = 0; e < kPer; e++)
+    if (key[e] != 0ull && (key[e] & hi_mask) == prefix)
+      atomicAdd(&lh[static_cast<uint32_t>(key[e] >> shift) & ((1u << width) - 1u)], 1u);
+  __syncthreads();
+}
+
+// Workgroups go to the XCDs in turn (block b to XCD b % 8), and XCDs 0 and 1
+// start a launch's workgroups about 2 us before the others.  With `packed`
+// the grid is ceil(tiles / 2) * 8 workgroups and only blocks b % 8 < 2 take
+// tiles (b / 8 * 2 + b % 8); the rest return at once.  Placement only: every
+// exchange between tiles is coherent across the whole device.
+__global__ __launch_bounds__(kReduceBlock) void topk_reduce_all_kernel(
+    float* out_scores, uint32_t* out_ids, const float* in_scores, const uint32_t* in_ids,
+    uint32_t count, uint32_t out_n, uint8_t* work_bytes, uint32_t tiles, uint32_t packed) {
+  const uint32_t tile = packed ? (blockIdx.x >> 3) * 2u + (blockIdx.x & 7u) : blockIdx.x;
+  if ((packed && (blockIdx.x & 7u) >= 2u) || tile >= tiles) return;
+  constexpr uint32_t kPer = kReduceTile / kReduceBlock;  // entries per thread
+  constexpr uint32_t kWaves = kReduceBlock / kWave;
+  constexpr uint32_t kSweep = 4u;   // entries a wave ranks in one pass over the list
+  constexpr uint32_t kUnroll = 4u;  // list entries a lane reads at once in that pass
+  __shared__ uint64_t s_key[kReduceAllList];  // digit histogram, then the ranked entries
+  __shared__ uint32_t s_bits[kReduceAllList];  // counts, then the tile map, then score bits
+  __shared__ uint32_t s_off[kReduceAllMaxTiles + 1u];
+  __shared__ uint32_t s_wave[kWaves];
+  __shared__ uint32_t s_sel[3];
+  __shared__ uint32_t s_n;
+  __shared__ uint32_t s_tag;
+  __shared__ uint64_t s_max;
+  uint32_t* const lh = reinterpret_cast<uint32_t*>(s_key);
+  static_assert(kReduceAllBuckets * sizeof(uint32_t) <= sizeof(s_key), "histogram in LDS");
+  static_assert(kReduceAllList % (kUnroll * kWave) == 0u, "padded list");
+  static_assert(kReduceAllMaxTiles <= kReduceAllList, "counts in s_bits");
+  ReduceAllWork* const work = reinterpret_cast<ReduceAllWork*>(work_bytes);
+  uint32_t* const hist = reinterpret_cast<uint32_t*>(work_bytes + kReduceAllHistOffset);
+  uint64_t* const list_comp = reinterpret_cast<uint64_t*>(work_bytes + kReduceAllListOffset);
+  uint32_t* const list_bits = reinterpret_cast<uint32_t*>(list_comp + kReduceAllList);
+  uint64_t* const slot_bound = reinterpret_cast<uint64_t*>(work_bytes + kReduceAllSlotOffset);
+  uint64_t* const slot_tag = slot_bound + tiles;
+  uint64_t* const region_comp = slot_tag + tiles;
+  uint32_t* const region_bits = reinterpret_cast<uint32_t*>(region_comp + uint64_t{tiles} * kReduceAllRegion);
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & (kWave - 1u);
+  const uint32_t wave = tid / kWave;
+  const uint32_t base = tile * kReduceTile;
+  const uint32_t n = min(kReduceTile, count - base);
+  uint64_t key[kPer];  // 0 past the tile's entries; 1 for padding ids
+  uint32_t sbits[kPer];
+  FG_RDTR(tile, 0);
+  // The call counter and the second route's barrier generation, read before
+  // this workgroup publishes anything.
+  uint32_t gen = 0u;
+  if (tid == 0u) {
+    gen = load_agent(&work->gen);
+    s_tag = load_agent(&work->call) + 1u;
+  }
+  {
+    uint32_t ids[kPer];
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; e++) {
+      const uint32_t i = min(e * kReduceBlock + tid, n - 1u);
+      sbits[e] = __float_as_uint(in_scores[base + i]);
+      ids[e] = in_ids ? in_ids[base + i] : base + i;
+    }
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; e++) {
+      const uint32_t i = e * kReduceBlock + tid;
+      key[e] = i >= n ? 0ull
+                      : (ids[e] == kInvalidId ? 1ull : greedy_comp(__uint_as_float(sbits[e]), ids[e]));
+    }
+  }
+  FG_RDTR(tile, 1);
+
+  // ---- 1: this tile's top K (at least) published ----
+  {
+    // K: the tile's even share of the 512, three binomial standard
+    // deviations and a margin; every entry of a single tile.
+    const uint32_t share = (out_n + tiles - 1u) / tiles;
+    const uint32_t spread = static_cast<uint32_t>(ceilf(3.0f * sqrtf(static_cast<float>(share))));
+    const uint32_t k = min(tiles == 1u ? out_n : min(share + spread + kReduceAllSlack, kReduceKeep), n);
+    uint64_t prefix = 0ull;  // ends as v_t: exactly the k-th largest composite
+    uint32_t fixed = 0u, above = 0u;
+    for (;;) {
+      const uint32_t width = min(kReduceAllDigit, 64u - fixed);
+      digit_hist(lh, key, prefix, fixed, width);
+      if (fixed == 0u) FG_RDTR(tile, 10);
+      top_bucket([&](uint32_t b) { return lh[b]; }, k - above, s_wave, s_sel);
+      if (fixed == 0u) FG_RDTR(tile, 11);
+      const uint64_t d = s_sel[0];
+      const uint32_t before = s_sel[1], in_bucket = s_sel[2];
+      __syncthreads();  // s_sel, s_wave and the histogram are written again
+      fixed += width;
+      prefix |= d << (64u - fixed);
+      above += before;
+      if (fixed == 64u) break;
+      if (in_bucket <= kWave) {
+        // The (k - above)-th largest of the boundary bucket's entries.
+        uint64_t* const cand = s_key;
+        const uint64_t mask = ~0ull << (64u - fixed);
+        if (tid == 0u) s_n = 0u;
+        __syncthreads();
+#pragma unroll
+        for (uint32_t e = 0; e < kPer; e++) {
+          const bool in = key[e] != 0ull && (key[e] & mask) == prefix;
+          const uint64_t m = ballot(in);
+          if (m == 0ull) continue;
+          const uint32_t leader = static_cast<uint32_t>(__builtin_ctzll(m));
+          uint32_t first = 0u;
+          if (lane == leader) first = atomicAdd(&s_n, static_cast<uint32_t>(__popcll(m)));
+          first = readlane32(first, leader);
+          if (in) cand[first + lanes_below(m)] = key[e];
+        }
+        __syncthreads();
+        FG_RDTR(tile, 12);
+        if (wave == 0u) {
+          // Lane l's candidate is the r-th largest (from 0) when fewer than
+          // r + 1 candidates exceed it and more than r reach it.
+          const uint64_t c = lane < in_bucket ? cand[lane] : 0ull;
+          const uint32_t r = k - above - 1u;
+          uint32_t gt = 0u, ge = 0u;
+#pragma unroll 8
+          for (uint32_t i = 0; i < in_bucket; i++) {
+            const uint64_t x = cand[i];
+            gt += x > c ? 1u : 0u;
+            ge += x >= c ? 1u : 0u;
+          }
+          if (lane < in_bucket && gt <= r && r < ge) s_max = c;
+        }
+        __syncthreads();
+        prefix = s_max;
+        break;
+      }
+    }
+    FG_RDTR(tile, 7);
+    if (tid == 0u) s_n = 0u;
+    __syncthreads();
+    uint64_t* const rc = region_comp + uint64_t{tile} * kReduceAllRegion;
+    uint32_t* const rb = region_bits + uint64_t{tile} * kReduceAllRegion;
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; e++) {
+      const bool keep = key[e] != 0ull && key[e] >= prefix;
+      const uint64_t m = ballot(keep);
+      if (m == 0ull) continue;
+      const uint32_t leader = static_cast<uint32_t>(__builtin_ctzll(m));
+      uint32_t first = 0u;
+      if (lane == leader) first = atomicAdd(&s_n, static_cast<uint32_t>(__popcll(m)));
+      first = readlane32(first, leader);
+      const uint32_t at = first + lanes_below(m);
+      if (keep && at < kReduceAllRegion) {
+        __hip_atomic_store(&rc[at], key[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&rb[at], sbits[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (tid == 0u) __hip_atomic_store(&slot_bound[tile], prefix, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#ifdef FG_REDUCE_TRACE
+    if (threadIdx.x == 0 && tile < 512u) g_reduce_trace[tile * 32u + 13u] = __builtin_amdgcn_s_memrealtime();
+#endif
+    wait_memory();  // every store of this workgroup acknowledged ...
+    __syncthreads();
+    if (tid == 0u)  // ... before the slot says they are there
+      __hip_atomic_store(&slot_tag[tile], (uint64_t{s_tag} << 32) | s_n, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  FG_RDTR(tile, 2);
+
+  // ---- 2: every slot tagged; the published entries at or above V gathered ----
+  if (wave == 0u) {
+    const uint32_t tag = s_tag;
+    for (uint32_t t0 = 0; t0 < tiles; t0 += kWave) {
+      const uint32_t t = t0 + lane;
+      bool ok = t >= tiles;
+      uint64_t v = 0ull;
+      for (;;) {
+        if (!ok) {
+          v = load_agent64(&slot_tag[t]);
+          ok = static_cast<uint32_t>(v >> 32) == tag;
+        }
+        if (ballot(!ok) == 0ull) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (t < tiles) s_bits[t] = static_cast<uint32_t>(v);
+    }
+  }
+  if (tid == 0u) s_max = 0ull;
+  __syncthreads();
+  FG_RDTR(tile, 3);
+  if (tile == 0u && tid == 0u)  // every workgroup has read the call counter
+    __hip_atomic_store(&work->call, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t M;
+  bool complete;
+  {
+    // The bounds' loads stay in flight over the offsets' scan.
+    uint64_t vb[kReduceAllMaxTiles / kReduceBlock];
+#pragma unroll
+    for (uint32_t u = 0; u < kReduceAllMaxTiles / kReduceBlock; u++) {
+      const uint32_t t = u * kReduceBlock + tid;
+      vb[u] = t < tiles ? load_agent64(&slot_bound[t]) : 0ull;
+    }
+    uint32_t over = 0u;
+    for (uint32_t t0 = 0; t0 < tiles; t0 += kReduceBlock) {
+      const uint32_t t = t0 + tid;
+      const uint32_t c = t < tiles ? s_bits[t] : 0u;
+      over |= c > kReduceAllRegion ? 1u : 0u;
+      const uint32_t incl = wave_prefix_sum_u32(c);
+      if (lane == kWave - 1u) s_wave[wave] = incl;
+      lds_barrier();
+      uint32_t start = (t0 ? s_off[t0] : 0u) + incl - c;
+#pragma unroll
+      for (uint32_t w = 0; w < kWaves; w++) start += w < wave ? s_wave[w] : 0u;
+      lds_barrier();
+      if (t < tiles) s_off[t + 1u] = start + c;
+      if (t0 == 0u && tid == 0u) s_off[0] = 0u;
+      lds_barrier();
+    }
+    M = s_off[tiles];
+    const uint32_t wave_over = ballot(over != 0u) != 0ull ? 1u : 0u;
+    if (lane == 0u) s_wave[wave] = wave_over;
+    lds_barrier();
+    over = M > kReduceAllList ? 1u : 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; w++) over |= s_wave[w];
+    complete = false;
+    FG_RDTR(tile, 8);
+    if (!over) {
+      lds_barrier();  // s_wave read by every wave
+      // s_bits maps each published entry to its tile, then holds score bits.
+      for (uint32_t t = wave; t < tiles; t += kWaves)
+        for (uint32_t i = s_off[t] + lane; i < s_off[t + 1u]; i += kWave) s_bits[i] = t;
+      lds_barrier();
+      // Wave w loads entries [w P, w P + P), P = M / 8 rounded up to 64.
+      constexpr uint32_t kLoads = kReduceAllList / kReduceBlock;
+      const uint32_t P = ((M + kWaves - 1u) / kWaves + kWave - 1u) & ~(kWave - 1u);
+      const uint32_t lo = min(wave * P, M), hi = min(lo + P, M);
+      uint64_t x[kLoads];
+      uint32_t xb[kLoads];
+#pragma unroll
+      for (uint32_t u = 0; u < kLoads; u++) {
+        const uint32_t j = lo + u * kWave + lane;
+        x[u] = 0ull;
+        xb[u] = 0u;
+        if (j < hi) {
+          const uint32_t t = s_bits[j];
+          const uint64_t at = uint64_t{t} * kReduceAllRegion + (j - s_off[t]);
+          x[u] = load_agent64(&region_comp[at]);
+          xb[u] = load_agent(&region_bits[at]);
+        }
+      }
+      uint64_t vmax = 0ull;
+#pragma unroll
+      for (uint32_t u = 0; u < kReduceAllMaxTiles / kReduceBlock; u++) vmax = vb[u] > vmax ? vb[u] : vmax;
+      vmax = wave_max_u64(vmax);
+      if (lane == 0u) atomicMax(reinterpret_cast<unsigned long long*>(&s_max), vmax);
+      __syncthreads();  // V known; every tile map entry read
+      const uint64_t V = s_max;
+      uint32_t kept = 0u;
+#pragma unroll
+      for (uint32_t u = 0; u < kLoads; u++) kept += __popcll(ballot(x[u] != 0ull && x[u] >= V));
+      if (lane == 0u) s_wave[wave] = kept;
+      FG_RDTR(tile, 9);
+      lds_barrier();
+      uint32_t pos = 0u, total = 0u;
+#pragma unroll
+      for (uint32_t w = 0; w < kWaves; w++) {
+        pos += w < wave ? s_wave[w] : 0u;
+        total += s_wave[w];
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kLoads; u++) {
+        const bool keep = x[u] != 0ull && x[u] >= V;
+        const uint64_t m = ballot(keep);
+        if (keep) {
+          s_key[pos + lanes_below(m)] = x[u];
+          s_bits[pos + lanes_below(m)] = xb[u];
+        }
+        pos += __popcll(m);
+      }
+      M = total;
+      complete = total >= out_n;
+    }
+  }
+  FG_RDTR(tile, 4);
+
+  if (!complete) {
+    // ---- second route: radix select over the whole input ----
+    uint64_t prefix = 0ull;
+    uint32_t fixed = 0u, above = 0u, round = 0u;
+    uint64_t T = 0ull;
+    bool capped = false;
+    __syncthreads();  // every wave is past its reads of s_wave and the tile map
+    for (;; round++) {
+      const uint32_t width = min(kReduceAllDigit, 64u - fixed);
+      uint32_t* const gh = hist + round * kReduceAllBuckets;
+      digit_hist(lh, key, prefix, fixed, width);
+#pragma unroll
+      for (uint32_t j = 0; j < kReduceAllBuckets / kReduceBlock; j++) {
+        const uint32_t c = lh[j * kReduceBlock + tid];
+        if (c) __hip_atomic_fetch_add(&gh[j * kReduceBlock + tid], c, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+      }
+      grid_sync(work, tiles, gen);
+      if (round) {  // every workgroup has read the previous round's table
+        uint32_t* const prev = hist + (round - 1u) * kReduceAllBuckets;
+        for (uint32_t i = tile * kReduceBlock + tid; i < kReduceAllBuckets; i += tiles * kReduceBlock)
+          __hip_atomic_store(&prev[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      top_bucket([&](uint32_t b) { return load_agent(&gh[b]); }, out_n - above, s_wave, s_sel);
+      const uint64_t d = s_sel[0];
+      const uint32_t before = s_sel[1], in_bucket = s_sel[2];
+      __syncthreads();
+      fixed += width;
+      prefix |= d << (64u - fixed);
+      const bool fits = above + before + in_bucket <= kReduceAllList;
+      above += before;
+      if (fits || fixed == 64u) {
+        T = prefix;
+        capped = !fits;
+        break;
+      }
+    }
+    const uint32_t tie_room = out_n - above;
+#pragma unroll
+    for (uint32_t e = 0; e < kPer; e++) {
+      bool keep = key[e] != 0ull && key[e] >= T;
+      if (capped && keep && key[e] == T) keep = atomicAdd(&work->ties, 1u) < tie_room;
+      const uint64_t m = ballot(keep);
+      if (m == 0ull) continue;
+      const uint32_t leader = static_cast<uint32_t>(__builtin_ctzll(m));
+      uint32_t first = 0u;
+      if (lane == leader) first = atomicAdd(&work->listed, static_cast<uint32_t>(__popcll(m)));
+      first = readlane32(first, leader);
+      if (keep) {
+        const uint32_t at = first + lanes_below(m);
+        __hip_atomic_store(&list_comp[at], key[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&list_bits[at], sbits[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    grid_sync(work, tiles, gen);
+    uint32_t* const last = hist + round * kReduceAllBuckets;
+    for (uint32_t i = tile * kReduceBlock + tid; i < kReduceAllBuckets; i += tiles * kReduceBlock)
+      __hip_atomic_store(&last[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    M = load_agent(&work->listed);
+    for (uint32_t j = tid; j < M; j += kReduceBlock) {
+      s_key[j] = load_agent64(&list_comp[j]);
+      s_bits[j] = load_agent(&list_bits[j]);
+    }
+    grid_sync(work, tiles, gen);  // every workgroup has read the list's length
+    if (tile == 0u && tid == 0u) {
+      __hip_atomic_store(&work->listed, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&work->ties, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // Zeros past the list to a multiple of kUnroll * 64 (a zero composite
+  // ranks no entry: every listed composite is at least 1).
+  const uint32_t padded = (M + kUnroll * kWave - 1u) & ~(kUnroll * kWave - 1u);
+  for (uint32_t j = M + tid; j < padded; j += kReduceBlock) s_key[j] = 0ull;
+  __syncthreads();
+  FG_RDTR(tile, 5);
+
+  // ---- 3: places; wave w of workgroup g ranks entries g + tiles * (w + 8 i) ----
+  const uint32_t stride = tiles * kWaves;
+  for (uint32_t j0 = tile + tiles * wave; j0 < M; j0 += kSweep * stride) {
+    uint64_t e[kSweep];
+    uint32_t jq[kSweep], gt[kSweep], ge[kSweep];
+#pragma unroll
+    for (uint32_t q = 0; q < kSweep; q++) {
+      jq[q] = j0 + q * stride;
+      e[q] = jq[q] < M ? s_key[jq[q]] : ~0ull;
+      gt[q] = 0u;
+      ge[q] = 0u;
+    }
+    for (uint32_t i0 = 0; i0 < padded; i0 += kUnroll * kWave) {
+      uint64_t x[kUnroll];
+#pragma unroll
+      for (uint32_t u = 0; u < kUnroll; u++) x[u] = s_key[i0 + u * kWave + lane];
+#pragma unroll
+      for (uint32_t u = 0; u < kUnroll; u++) {
+#pragma unroll
+        for (uint32_t q = 0; q < kSweep; q++) {
+          gt[q] += x[u] > e[q] ? 1u : 0u;
+          ge[q] += x[u] >= e[q] ? 1u : 0u;
+        }
+      }
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kSweep; q++) {
+      uint32_t rank = wave_reduce_sum_u32(gt[q]);
+      if (wave_reduce_sum_u32(ge[q]) > rank + 1u && jq[q] < M) {
+        // Copies of this composite (duplicate ids): those listed first rank first.
+        uint32_t before = 0u;
+        for (uint32_t i = lane; i < jq[q]; i += kWave) before += s_key[i] == e[q] ? 1u : 0u;
+        rank += wave_reduce_sum_u32(before);
+      }
+      if (lane == 0u && jq[q] < M && rank < out_n) {
+        out_scores[rank] = __uint_as_float(s_bits[jq[q]]);
+        out_ids[rank] = e[q] == 1ull ? kInvalidId : ~static_cast<uint32_t>(e[q]);
+      }
+    }
+  }
+  FG_RDTR(tile, 6);
 }
 
 }  // namespace fg

@@ -36,6 +36,7 @@ EXPORTS = (
     "fg_sampler_state_init", "fg_sampler_uniform", "fg_sampler_select",
     "fg_sampler_penalties_active", "fg_sampler_apply_penalties",
     "fg_hip_apply_penalties", "fg_hip_argmax_reduce", "fg_hip_topk_select", "fg_hip_topk_reduce",
+    "fg_hip_topk_reduce_all", "fg_hip_topk_reduce_all_workspace_bytes",
     "fg_hip_history_build", "fg_hip_history_build_wire",
     "fg_output_history_encode", "fg_output_history_encode_vocab",
     "fg_output_history_decode", "fg_output_history_decode_vocab",
@@ -145,6 +146,8 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_hip_argmax_reduce": (C.c_int, [P, P, P, P, u32, C.POINTER(u32), P, E]),
         "fg_hip_topk_select": (C.c_int, [P, P, P, P, u32, u32, C.POINTER(u32), P, E]),
         "fg_hip_topk_reduce": (C.c_int, [P, P, P, P, u32, C.POINTER(u32), P, E]),
+        "fg_hip_topk_reduce_all": (C.c_int, [P, P, P, P, u32, P, C.POINTER(u32), P, E]),
+        "fg_hip_topk_reduce_all_workspace_bytes": (u64, [u32]),
         "fg_hip_history_build": (C.c_int, [P, u64, u32, P, P, u32, P, P, E]),
         "fg_hip_history_build_wire": (C.c_int, [P, u64, u32, P, P, u32, P, P, P, E]),
         "fg_output_history_encode": (C.c_int, [P, u32, C.POINTER(u32), C.POINTER(OutputHistory), E]),
@@ -270,6 +273,22 @@ def topk_reduce(out_scores, out_ids, in_scores, in_ids, count, stream=None) -> i
     _check(lib().fg_hip_topk_reduce(_ptr(out_scores), _ptr(out_ids), _ptr(in_scores),
                                     _ptr(in_ids), count, C.byref(n), _stream(stream),
                                     C.byref(err)), err)
+    return n.value
+
+
+def topk_reduce_all_workspace_bytes(count) -> int:
+    """fg_hip_topk_reduce_all_workspace_bytes: the workspace for `count` scores."""
+    return int(lib().fg_hip_topk_reduce_all_workspace_bytes(count))
+
+
+def topk_reduce_all(out_scores, out_ids, in_scores, in_ids, count, workspace,
+                    stream=None) -> int:
+    """fg_hip_topk_reduce_all: the whole top-512 scan in one launch; returns the output count."""
+    err = FgError()
+    n = C.c_uint32(0)
+    _check(lib().fg_hip_topk_reduce_all(_ptr(out_scores), _ptr(out_ids), _ptr(in_scores),
+                                        _ptr(in_ids), count, _ptr(workspace), C.byref(n),
+                                        _stream(stream), C.byref(err)), err)
     return n.value
 
 

@@ -89,6 +89,26 @@ fg_status fg_hip_topk_reduce(float *output_scores, uint32_t *output_ids,
                              uint32_t count, uint32_t *output_count, void *stream,
                              fg_error *err);
 
+/* The whole QSA top-512 scan in one launch (no counterpart entry point in
+ * the reference, which iterates fg_vk_topk_reduce, src/qsa.c:839-851): the
+ * top min(count, 512) entries of the input in the comparator order of
+ * fg_hip_topk_reduce, sorted, as the reference's loop leaves them;
+ * *output_count = min(count, 512).  in_ids == NULL means ids 0..count-1.
+ * `workspace`: fg_hip_topk_reduce_all_workspace_bytes(count) bytes of
+ * device memory, 256-byte aligned, zero before the first call with it.
+ * Bytes 4-7 and 16-19 hold a barrier generation and a call counter that
+ * calls advance; each call returns the rest of the first 98,368 bytes
+ * (counters and tables) to zero and writes what else it reads.  Calls that share a workspace must not
+ * overlap.
+ * FG_ERR_LIMIT when the count's 4096-entry tiles are more than 1024 or more
+ * workgroups than the device holds at once (262,144 scores are 64 tiles).
+ * Errors: count == 0, null pointers. */
+uint64_t fg_hip_topk_reduce_all_workspace_bytes(uint32_t count);
+fg_status fg_hip_topk_reduce_all(float *output_scores, uint32_t *output_ids,
+                                 const float *input_scores, const uint32_t *input_ids,
+                                 uint32_t count, void *workspace, uint32_t *output_count,
+                                 void *stream, fg_error *err);
+
 /* Dense history count tables from token lists, one launch, stream-ordered,
  * no synchronisation: for each row r, counts[r*stride .. +vocab) is cleared
  * and then incremented once per id in ids[offsets[r] .. offsets[r+1])

@@ -46,7 +46,19 @@ def test_argument_errors_without_device_work():
     assert lib.fg_sampler_hip_sample(None, None, None, C.byref(err)) == 2
     assert lib.fg_sampler_hip_set_configs(None, None, 0, 0, None, C.byref(err)) == 2
     assert lib.fg_hip_history_build(None, 0, 0, None, None, 0, None, None, C.byref(err)) == 2
+    assert lib.fg_hip_topk_reduce_all(None, None, None, None, 5, None, C.byref(n), None,
+                                      C.byref(err)) == 2
     lib.fg_sampler_hip_destroy(None)
+
+
+def test_reduce_all_workspace_bytes():
+    """Fixed part (header, six 4096-bucket tables, a 6144-entry list), then per
+    4096-score tile an 8-byte bound, an 8-byte slot and a 1024-entry region of
+    12-byte entries."""
+    fixed = 64 + 6 * 4096 * 4 + 6144 * 12
+    for count, tiles in ((1, 1), (4096, 1), (4097, 2), (262_144, 64), (300_000, 74)):
+        want = fixed + tiles * 16 + tiles * 1024 * 12
+        assert fg_hip.topk_reduce_all_workspace_bytes(count) == want
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -454,6 +454,137 @@ def test_topk_reduce_ladder_gives_sorted_top512(dev):
     assert np.array_equal(got, ids[want])
 
 
+def _reduce_all(dev, scores, ids, work):
+    import torch
+    n = scores.size
+    os_ = torch.full((512,), 7.0, dtype=torch.float32, device=dev)
+    oi = torch.full((512,), 7, dtype=torch.int32, device=dev)
+    got = fg_hip.topk_reduce_all(os_, oi, dev_f32(scores, dev),
+                                 None if ids is None else dev_u32(ids, dev), n, work)
+    torch.cuda.synchronize()
+    return os_.cpu().numpy()[:got], oi.cpu().numpy().view(np.uint32)[:got], got
+
+
+_REDUCE_ALL_ZEROED = 64 + 6 * 4096 * 4  # header and digit tables; the list is not read past its count
+
+
+def _zeroed(work):
+    """The counters and tables are zero after a call; bytes 4-7 and 16-19 hold
+    the barrier generation and the call counter."""
+    head = work[:_REDUCE_ALL_ZEROED].clone()
+    head[4:8] = 0
+    head[16:20] = 0
+    return int(head.count_nonzero()) == 0
+
+
+def _reduce_all_work(dev, count):
+    import torch
+    return torch.zeros(fg_hip.topk_reduce_all_workspace_bytes(count), dtype=torch.uint8, device=dev)
+
+
+def _check_top(scores, ids, gs, gi, got):
+    """The first min(count, 512) entries in comparator order (padding ids,
+    which tie among themselves, compared as a set)."""
+    want = np.lexsort(O.reduce_order_key(scores, ids))[:min(scores.size, 512)]
+    assert got == want.size
+    wi, ws = ids[want], scores[want]
+    real = wi != 0xFFFFFFFF
+    assert np.array_equal(gi[real], wi[real])
+    assert np.array_equal(gs[real].view(np.uint32), ws[real].view(np.uint32))
+    assert np.array_equal(gi == 0xFFFFFFFF, ~real)
+
+
+def test_topk_reduce_all_matches_the_ladder(dev):
+    """One launch against the per-level ladder it replaces (src/qsa.c:839-851)
+    on the same 300,000 scores with NaNs: the same 512 entries in the same
+    order, bit-exact."""
+    import torch
+    rng = np.random.default_rng(3)
+    count = 300_000
+    s = rng.normal(0, 1, count).astype(np.float32)
+    s[rng.integers(0, count, 50)] = np.nan
+    ids = np.arange(count, dtype=np.uint32)
+    cur_s, cur_i, n = dev_f32(s, dev), dev_u32(ids, dev), count
+    while n > 512:
+        cap = ((n + 4095) // 4096) * 512
+        ns = torch.empty(cap, dtype=torch.float32, device=dev)
+        ni = torch.empty(cap, dtype=torch.int32, device=dev)
+        n = fg_hip.topk_reduce(ns, ni, cur_s, cur_i, n)
+        cur_s, cur_i = ns, ni
+    work = _reduce_all_work(dev, count)
+    gs, gi, got = _reduce_all(dev, s, None, work)
+    assert got == 512
+    assert np.array_equal(gi, cur_i.cpu().numpy().view(np.uint32)[:512])
+    assert np.array_equal(gs.view(np.uint32), cur_s.cpu().numpy()[:512].view(np.uint32))
+    _check_top(s, ids, gs, gi, got)
+    assert _zeroed(work), "workspace not returned to zero"
+
+
+@pytest.mark.parametrize("count", [1, 7, 511, 512, 513, 4096, 4097, 20_000, 151_936, 262_144])
+def test_topk_reduce_all_matches_oracle(dev, count):
+    """NaN payloads, +-Inf, quantised ties, scattered ids with some padding
+    ids, partial last tiles and counts under 512; one workspace reused by
+    two calls, the second smaller."""
+    rng = np.random.default_rng(count + 1)
+    work = _reduce_all_work(dev, count)
+    for n in (count, max(1, count // 3)):
+        s = (np.round(rng.normal(0, 3, n) * 4) / 4).astype(np.float32)
+        s[rng.random(n) < 0.01] = np.float32(np.nan)
+        s.view(np.uint32)[rng.random(n) < 0.005] = 0x7FC00123
+        s[rng.random(n) < 0.005] = np.inf
+        s[rng.random(n) < 0.005] = -np.inf
+        ids = rng.permutation(n * 3)[:n].astype(np.uint32)
+        ids[rng.random(n) < 0.01] = 0xFFFFFFFF
+        gs, gi, got = _reduce_all(dev, s, ids, work)
+        _check_top(s, ids, gs, gi, got)
+    assert _zeroed(work)
+
+
+@pytest.mark.parametrize("kind", ["equal", "duplicate_ids", "sorted", "one_tile_high"])
+def test_topk_reduce_all_adversarial(dev, kind):
+    """Inputs that defeat the tile bounds: every score equal (ids decide),
+    entries repeated with the same id, ascending scores (the last tile holds
+    the whole answer), one tile far above the rest."""
+    rng = np.random.default_rng(11)
+    count = 100_000
+    ids = np.arange(count, dtype=np.uint32)
+    if kind == "equal":
+        s = np.full(count, 2.5, dtype=np.float32)
+        ids = rng.permutation(count).astype(np.uint32)
+    elif kind == "duplicate_ids":
+        s = (np.round(rng.normal(0, 1, count)) + 0.5).astype(np.float32)
+        ids = rng.integers(0, 700, count).astype(np.uint32)
+    elif kind == "sorted":
+        s = np.sort(rng.normal(0, 1, count)).astype(np.float32)
+    else:
+        s = rng.normal(0, 1, count).astype(np.float32)
+        s[8192:12288] += 100
+    work = _reduce_all_work(dev, count)
+    gs, gi, got = _reduce_all(dev, s, ids, work)
+    if kind == "duplicate_ids":
+        # identical (score, id) entries tie: compare the ordered pairs
+        want = np.lexsort(O.reduce_order_key(s, ids))[:512]
+        assert got == 512
+        assert np.array_equal(gi, ids[want])
+        assert np.array_equal(gs, s[want])
+    else:
+        _check_top(s, ids, gs, gi, got)
+    assert _zeroed(work)
+
+
+def test_topk_reduce_all_limits(dev):
+    import torch
+    x = torch.zeros(8, device=dev)
+    w = torch.zeros(256, dtype=torch.uint8, device=dev)
+    with pytest.raises(fg_hip.FgStatusError) as e:
+        fg_hip.topk_reduce_all(x, x, x, None, 0, w)
+    assert e.value.code == fg_hip.FG_ERR_ARGUMENT
+    big = 1 << 26  # 16,384 tiles: more workgroups than the device holds at once
+    with pytest.raises(fg_hip.FgStatusError) as e:
+        fg_hip.topk_reduce_all(x, x, x, None, big, w)
+    assert e.value.code == fg_hip.FG_ERR_LIMIT
+
+
 def test_topk_reduce_argument_errors(dev):
     import torch
     x = torch.zeros(8, device=dev)
