@@ -94,7 +94,8 @@ struct SampleArgs {
   // workspace, indexed by wave slot = (row * chunks + chunk) * kWaves + wave
   uint64_t* cand;        // [slot][kMaxK] top-kk composites of the wave, descending, 0 = empty
   uint64_t* greedy;      // [slot] greedy composite
-  uint32_t* spec;        // [slot] the wave's speculative stream key (0 = none)
+  uint64_t* spec;        // [slot] the wave's speculative stream key (0 = none; a
+                         // tagged word in the finisher hand-off)
   double* lse;           // [slot][2] (max s, sum exp((s - max)/T))
   double* zsum;          // [slot][3] whole-row nucleus mass (max, sum, error bound)
   uint32_t* row_done;    // [rows * kLineWords] arrivals, one cache line per row,
@@ -1024,7 +1025,9 @@ __device__ __forceinline__ uint32_t spec_key(const SampleArgs& a, uint32_t row, 
                                              const uint32_t* ks_lds) {
   const uint32_t n = a.chunks * static_cast<uint32_t>(kWaves);
   if (i >= n) return 0u;
-  return a.chunks == 1u ? ks_lds[i] : load_coherent(a.spec + static_cast<uint64_t>(row) * n + i);
+  return a.chunks == 1u
+             ? ks_lds[i]
+             : static_cast<uint32_t>(load_coherent(a.spec + static_cast<uint64_t>(row) * n + i));
 }
 
 __device__ inline uint64_t spec_check(const SampleArgs& a, const RowParams& p, uint32_t row,
@@ -1157,14 +1160,47 @@ __device__ __forceinline__ void rank_place(const uint64_t* lists, uint32_t strid
   if (e != 0ull && r < kk) out[r] = e;
 }
 
-// The finisher's eight lists in LDS (list c at lists + 32 c): lanes 0-31 of
-// wave w place the entries of list 2w, lanes 32-63 those of list 2w + 1.
-__device__ __forceinline__ void rank_place_lists(const uint64_t* lists, uint32_t wave,
-                                                 uint32_t kk, uint64_t* out) {
+// The same for lists of at most 64 entries (a six-step search; all 64
+// entries above e are told from 63 by the last entry).
+template <int kN>
+__device__ __forceinline__ void rank_place64(const uint64_t* lists, uint32_t stride, uint64_t e,
+                                             uint32_t kk, uint64_t* out) {
+  uint32_t lo[kN];
+#pragma unroll
+  for (int i = 0; i < kN; i++) lo[i] = lists[i * stride + 31u] > e ? 32u : 0u;
+#pragma unroll
+  for (uint32_t h = 16u; h >= 1u; h /= 2u) {
+#pragma unroll
+    for (int i = 0; i < kN; i++) lo[i] += lists[i * stride + lo[i] + h - 1u] > e ? h : 0u;
+  }
+  if (kk == 64u) {
+#pragma unroll
+    for (int i = 0; i < kN; i++) lo[i] += (lo[i] == 63u && lists[i * stride + 63u] > e) ? 1u : 0u;
+  }
+  uint32_t r = 0u;
+#pragma unroll
+  for (int i = 0; i < kN; i++) r += lo[i];
+  if (e != 0ull && r < kk) out[r] = e;
+}
+
+// The finisher's eight lists in LDS.  Lists of at most 32 (list c at
+// lists32 + 32 c): lanes 0-31 of wave w place the entries of list 2w, lanes
+// 32-63 those of list 2w + 1.  Longer lists (list c at lists64 + 64 c): wave
+// w places both lists' entries, a position per lane.
+__device__ __forceinline__ void rank_place_lists(const uint64_t* lists32, const uint64_t* lists64,
+                                                 uint32_t wave, uint32_t kk, uint64_t* out) {
   const uint32_t lane = lane_id();
-  const uint32_t c = 2u * wave + (lane >= 32u ? 1u : 0u);
-  const uint32_t pos = lane & 31u;
-  rank_place<8>(lists, 32u, pos < kk ? lists[c * 32u + pos] : 0ull, kk, out);
+  if (kk <= 32u) {
+    const uint32_t c = 2u * wave + (lane >= 32u ? 1u : 0u);
+    const uint32_t pos = lane & 31u;
+    rank_place<8>(lists32, 32u, pos < kk ? lists32[c * 32u + pos] : 0ull, kk, out);
+  } else {
+#pragma unroll
+    for (uint32_t h = 0; h < 2u; h++) {
+      const uint32_t c = 2u * wave + h;
+      rank_place64<8>(lists64, 64u, lane < kk ? lists64[c * 64u + lane] : 0ull, kk, out);
+    }
+  }
 }
 
 }  // namespace fg
@@ -1178,6 +1214,7 @@ namespace fg {
 template <class F>
 __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
   __shared__ uint64_t s_buf[F::kTop ? kWaves : 1][F::kTop ? kCap + kWave : 1];
+  static_assert(!F::kTop || kWaves * (kCap + kWave) >= 8u * kMaxK, "finisher lists in s_buf");
   __shared__ uint64_t s_top[kWaves][kWave];
   __shared__ uint64_t s_greedy[kWaves];
   __shared__ uint32_t s_ks[kWaves];
@@ -1187,7 +1224,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
   __shared__ double s_nz[kWaves];
   __shared__ double s_ne[kWaves];
   __shared__ uint32_t s_wg_key;
-  __shared__ uint64_t s_rank[32];
+  __shared__ uint64_t s_rank[kWave];
   FG_TRACE_DECL;
   FG_TRACE_INIT;
 
@@ -1338,7 +1375,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
   if (F::kNuc && nuc) wmass = wave_mass_combine(static_cast<double>(st.nm), st.nz, st.ne);
 
   // ---- the workgroup's result: wave 0 combines the four waves from LDS ----
-  // Finisher protocol (launches whose rows all keep top lists of at most 32
+  // Finisher protocol (launches whose rows all keep top lists of at most 64
   // over 2-8 chunks, nothing else): one chunk finishes the row, reading the
   // other chunks' lists until every entry carries the tag; the others store
   // their lists tagged and end, with no wait for the stores and no arrival
@@ -1346,8 +1383,8 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
   // giving chunk 0 a longer slice, so that it would usually end last, cost
   // more stream time than the wait it saved).  All four waves of the
   // finishing workgroup rank the lists.
-  const bool fin_mode = F::kTop && !F::kSpec && !F::kLse && !F::kNuc && finisher_of(a) != 0u &&
-                        !greedy && kk != 0u && kk <= 32u && a.chunks <= 8u;
+  const bool fin_mode = F::kTop && !F::kLse && !F::kNuc && finisher_of(a) != 0u &&
+                        !greedy && kk != 0u && kk <= static_cast<uint32_t>(kMaxK) && a.chunks <= 8u;
   const bool fin_wg = fin_mode && a.chunks != 1u && chunk == finisher_of(a) - 1u;
   // The same for batches of greedy rows (no log-probs) over 2-64 chunks:
   // one composite per chunk.
@@ -1414,7 +1451,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
     if (F::kTop && fin_wg) {
       // The finisher's helpers: wave 0 fills the lists, all four rank them.
       __syncthreads();
-      rank_place_lists(&s_top[0][0], wave, kk, s_rank);
+      rank_place_lists(&s_top[0][0], &s_buf[0][0], wave, kk, s_rank);
       __syncthreads();
     }
     if constexpr (F::kNuc) nuc_tail(false, 0.0f);
@@ -1448,6 +1485,8 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
     const uint64_t header = wire_header(a.finisher >> 16u);
     if (fin_mode && lane < kk)
       store_coherent(a.cand + slot * kMaxK + lane, header | wire_payload(fin));
+    if (fin_mode && spec && lane < static_cast<uint32_t>(kWaves))
+      store_coherent(a.spec + slot * kWaves + lane, header | s_ks[lane]);
     if (gfin_mode && lane == 0) store_coherent(a.greedy + slot, header | greedy_payload(g));
     FG_TRACE(a, 3);
     FG_TRACE_FLUSH(a);
@@ -1458,7 +1497,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
       // Publish the workgroup's partials with device-coherent stores.
       if (F::kTop && kk && lane < kk) store_coherent(a.cand + slot * kMaxK + lane, fin);
       if (spec && lane < static_cast<uint32_t>(kWaves))
-        store_coherent(a.spec + slot * kWaves + lane, s_ks[lane]);
+        store_coherent(a.spec + slot * kWaves + lane, static_cast<uint64_t>(s_ks[lane]));
       if (lane == 0) {
         if (F::kGreedy && greedy) store_coherent(a.greedy + slot, g);
         if (lse) {
@@ -1493,26 +1532,36 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
       // below even when the wait gives up).
       const uint32_t own = finisher_of(a) - 1u;
       const uint64_t header = wire_header(a.finisher >> 16u);
+      // Lists of at most 32: lanes 0-31 hold list 2t, lanes 32-63 list
+      // 2t + 1 in x[t] (t < 4).  Longer lists: x[c] holds list c at
+      // position `lane`.
+      const bool wide = kk > 32u;
       const bool hi = lane >= 32u;
-      const uint32_t pos = lane & 31u;  // lanes 0-31: list 2t, 32-63: list 2t + 1
-      uint64_t x[4];
+      const uint32_t pos = wide ? lane : (lane & 31u);
+      uint64_t x[8];
+      auto list_of = [&](int t) -> uint32_t { return wide ? static_cast<uint32_t>(t) : 2u * t + (hi ? 1u : 0u); };
+      // Speculating rows: lane i also reads wave i's key (i < chunks * 4).
+      const uint32_t ks_chunk = lane / static_cast<uint32_t>(kWaves);
+      const bool ks_read = spec && ks_chunk < a.chunks && ks_chunk != own;
+      uint64_t y = header;
       auto fetch = [&]() {
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-          const uint32_t c = 2u * t + (hi ? 1u : 0u);
-          if (c != own && c < a.chunks && pos < kk)
+        for (int t = 0; t < 8; t++) {
+          const uint32_t c = list_of(t);
+          if ((wide || t < 4) && c != own && c < a.chunks && pos < kk)
             x[t] = load_coherent(a.cand + (row_slot + c) * kMaxK + pos);
         }
+        if (ks_read) y = load_coherent(a.spec + row_slot * kWaves + lane);
       };
 #pragma unroll
-      for (int t = 0; t < 4; t++) x[t] = header;
+      for (int t = 0; t < 8; t++) x[t] = header;
       fetch();
       FG_TRACE(a, 8);
       uint64_t t0 = 0ull;
       for (uint32_t spin = 0;; spin++) {
-        bool miss = false;
+        bool miss = !wire_current(y, header);
 #pragma unroll
-        for (int t = 0; t < 4; t++) miss |= !wire_current(x[t], header);
+        for (int t = 0; t < 8; t++) miss |= !wire_current(x[t], header);
         if (ballot(miss) == 0ull) break;
         if (wait_passed(a, spin, t0)) {
           gave_up = true;
@@ -1522,20 +1571,24 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
         fetch();
       }
       FG_TRACE(a, 4);
-      uint64_t* lists = &s_top[0][0];
+      uint64_t* const lists = wide ? &s_buf[0][0] : &s_top[0][0];
+      const uint32_t stride = wide ? 64u : 32u;
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const uint32_t c = 2u * t + (hi ? 1u : 0u);
-        if (c != own) lists[c * 32u + pos] = comp_of_payload(x[t] & kWirePayload);
+      for (int t = 0; t < 8; t++) {
+        const uint32_t c = list_of(t);
+        if ((wide || t < 4) && c != own) lists[c * stride + pos] = comp_of_payload(x[t] & kWirePayload);
       }
-      if (lane < 32u) {
-        lists[own * 32u + lane] = lane < kk ? fin : 0ull;
-        s_rank[lane] = 0ull;
+      if (wide || lane < 32u) lists[own * stride + lane] = lane < kk ? fin : 0ull;
+      s_rank[lane] = 0ull;
+      __syncthreads();
+      rank_place_lists(&s_top[0][0], &s_buf[0][0], 0u, kk, s_rank);
+      __syncthreads();
+      fin = lane < kk ? s_rank[lane] : 0ull;
+      if (spec) {
+        const uint32_t w = lane % static_cast<uint32_t>(kWaves);
+        ks0 = ks_chunk == own ? s_ks[w]
+              : ks_chunk < a.chunks ? static_cast<uint32_t>(y & kWirePayload) : 0u;
       }
-      __syncthreads();
-      rank_place_lists(lists, 0u, kk, s_rank);
-      __syncthreads();
-      fin = lane < 32u ? s_rank[lane] : 0ull;
       FG_TRACE(a, 5);
     } else if (F::kTop && kk) {
       if (kk <= 32u) {

@@ -269,7 +269,7 @@ struct Workspace {
   RowParams* params;        // [max_rows]
   uint64_t* cand;           // [slots][kMaxK]
   uint64_t* greedy;         // [slots]
-  uint32_t* spec;           // [slots] speculative stream keys
+  uint64_t* spec;           // [slots] speculative stream keys
   double* lse;              // [slots][2]
   double* zsum;             // [slots][3]
   uint32_t* row_done;       // [max_rows * kLineWords], zero between launches
@@ -317,7 +317,7 @@ constexpr size_t kOffParams = 0;
 constexpr size_t kOffCand = align256(kOffParams + sizeof(RowParams) * kStaticMaxRows);
 constexpr size_t kOffGreedy = align256(kOffCand + sizeof(uint64_t) * kStaticSlots * fg::kMaxK);
 constexpr size_t kOffSpec = align256(kOffGreedy + sizeof(uint64_t) * kStaticSlots);
-constexpr size_t kOffLse = align256(kOffSpec + sizeof(uint32_t) * kStaticSlots);
+constexpr size_t kOffLse = align256(kOffSpec + sizeof(uint64_t) * kStaticSlots);
 constexpr size_t kOffZsum = align256(kOffLse + sizeof(double) * kStaticSlots * 2u);
 constexpr size_t kOffDone = align256(kOffZsum + sizeof(double) * kStaticSlots * 3u);
 constexpr size_t kStaticBytes = align256(kOffDone + sizeof(uint32_t) * fg::kLineWords * kStaticMaxRows);
@@ -352,7 +352,7 @@ hipError_t static_workspace(Workspace* w) {
   w->params = reinterpret_cast<RowParams*>(p + kOffParams);
   w->cand = reinterpret_cast<uint64_t*>(p + kOffCand);
   w->greedy = reinterpret_cast<uint64_t*>(p + kOffGreedy);
-  w->spec = reinterpret_cast<uint32_t*>(p + kOffSpec);
+  w->spec = reinterpret_cast<uint64_t*>(p + kOffSpec);
   w->lse = reinterpret_cast<double*>(p + kOffLse);
   w->zsum = reinterpret_cast<double*>(p + kOffZsum);
   w->row_done = reinterpret_cast<uint32_t*>(p + kOffDone);
@@ -474,13 +474,14 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
   a.split = geo.split;
   uint32_t finisher = 0u;
   {
-    // Finisher protocol (see the kernel): every row a top list of at most 32
+    // Finisher protocol (see the kernel): every row a top list of at most 64
     // (no greedy row, no log-probs) over 2-8 chunks, or every row greedy (no
     // log-probs) over 2-64 chunks; ids that fit a tagged word.
     bool ok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= 8u && b->logprobs == 0u &&
               vocab <= fg::kWireVocab;
     for (uint32_t r = 0; ok && r < b->rows; r++)
-      ok = h_params[r].temperature > 0.0f && h_params[r].top_k >= 1u && h_params[r].top_k <= 32u;
+      ok = h_params[r].temperature > 0.0f && h_params[r].top_k >= 1u &&
+           h_params[r].top_k <= static_cast<uint32_t>(fg::kMaxK);
     bool gok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= fg::kMaxChunks &&
                b->logprobs == 0u && vocab <= fg::kWireVocab;
     for (uint32_t r = 0; gok && r < b->rows; r++) gok = h_params[r].temperature == 0.0f;
@@ -966,7 +967,7 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMemset(s->ws.cand, 0, sizeof(uint64_t) * slots * fg::kMaxK);
   if (e == hipSuccess) e = hipMalloc(&s->ws.greedy, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMemset(s->ws.greedy, 0, sizeof(uint64_t) * slots);
-  if (e == hipSuccess) e = hipMalloc(&s->ws.spec, sizeof(uint32_t) * slots);
+  if (e == hipSuccess) e = hipMalloc(&s->ws.spec, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.lse, sizeof(double) * slots * 2);
   if (e == hipSuccess) e = hipMalloc(&s->ws.zsum, sizeof(double) * slots * 3);
   const size_t done_bytes = sizeof(uint32_t) * fg::kLineWords * max_rows;

@@ -528,12 +528,15 @@ def test_paired_layout_shares(dev, monkeypatch, groups, share, k):
 
 @pytest.mark.parametrize("groups,finisher,k", [(32, "1", 20), (32, "2", 32), (64, "3", 1),
                                                (128, "1", 20), (128, "6", 32), (128, "8", 7),
-                                               (128, "0", 20), (256, "1", 20), (256, "1", 32)])
+                                               (128, "0", 20), (256, "1", 20), (256, "1", 32),
+                                               (32, "2", 33), (64, "4", 50), (128, "7", 64),
+                                               (128, "1", 50)])
 def test_finisher_rows(dev, monkeypatch, groups, finisher, k):
     """The finisher hand-off (one chunk of each row reads the others' tagged
     lists; FG_HIP_FINISHER=c+1 picks chunk c, 0 the last-arriver hand-off):
-    16 rows over 2, 4 or 8 chunks, finishing chunks whose list sits in the
-    low or the high (reversed) lanes, top values at slice edges and in one
+    16 rows over 2, 4 or 8 chunks, lists of 1-32 (two a register in the
+    finisher) and of 33-64 (a position per lane), finishing chunks whose list
+    sits in the low or the high (reversed) lanes, top values at slice edges and in one
     slice (16 chunks: more than the finisher takes, so the last-arriver
     hand-off runs, with the workgroups' rank merges); three calls on one sampler with new inputs each (the finisher
     clears the lists it reads, so a call sees none of the last one's).
