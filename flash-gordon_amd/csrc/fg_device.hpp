@@ -162,6 +162,33 @@ __device__ __forceinline__ uint64_t greedy_comp(float v, uint32_t id) {
 }
 __device__ __forceinline__ uint32_t greedy_id(uint64_t c) { return ~static_cast<uint32_t>(c); }
 
+// ---- tagged hand-off words ------------------------------------------------------
+// A word one workgroup stores for another to poll: bit 63 set, bits 62-50 an
+// epoch (1-8191), bits 49-0 a payload, 0 for nothing stored.  The reader polls
+// until the word carries the epoch it expects, so words are never cleared.
+constexpr uint32_t kWireIdBits = 18;
+constexpr uint32_t kWireVocab = 1u << kWireIdBits;  // ids below this travel in a word
+constexpr uint64_t kWirePayload = (1ull << 50) - 1ull;
+constexpr uint32_t kMaxEpoch = 8191;  // epochs 1..8191
+
+__device__ __forceinline__ uint64_t wire_header(uint32_t epoch) {
+  return (0x2000ull | epoch) << 50;
+}
+__device__ __forceinline__ bool wire_current(uint64_t w, uint64_t header) {
+  return (w >> 50) == (header >> 50);
+}
+// Greedy composite <-> payload (high word = greedy key, low word = ~id; ids
+// below kWireVocab): a larger payload is a larger composite.
+__device__ __forceinline__ uint64_t greedy_payload(uint64_t g) {
+  if (g == 0ull) return 0ull;
+  return ((g >> 32) << kWireIdBits) | static_cast<uint64_t>(kWireVocab - 1u - greedy_id(g));
+}
+__device__ __forceinline__ uint64_t greedy_of_payload(uint64_t w) {
+  if (w == 0ull) return 0ull;
+  const uint32_t id = kWireVocab - 1u - static_cast<uint32_t>(w & (kWireVocab - 1u));
+  return ((w >> kWireIdBits) << 32) | static_cast<uint64_t>(~id);
+}
+
 // Penalty of src/sampler.c:55-58 for one logit seen c > 0 times.  The kernels
 // are compiled with -ffp-contract=off so the product and the sum round
 // separately, and '/' is the IEEE-rounded f32 division.

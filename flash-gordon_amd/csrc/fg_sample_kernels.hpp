@@ -1066,18 +1066,8 @@ __device__ inline uint64_t spec_check(const SampleArgs& a, const RowParams& p, u
 // (larger vocabularies take the last-arriver hand-off).  A finisher that has
 // not seen every word after the launch's wait limit (a.wait_ticks of the
 // 100 MHz clock) reports kStTimeout for its row instead of a token.
-constexpr uint32_t kWireIdBits = 18;
-constexpr uint32_t kWireVocab = 1u << kWireIdBits;  // ids below this travel in a word
-constexpr uint64_t kWirePayload = (1ull << 50) - 1ull;
-constexpr uint32_t kMaxEpoch = 8191;  // epochs 1..8191
 constexpr int32_t kStTimeout = 7;     // FG_ERR_UNAVAILABLE: the finisher's wait gave up
 
-__device__ __forceinline__ uint64_t wire_header(uint32_t epoch) {
-  return (0x2000ull | epoch) << 50;
-}
-__device__ __forceinline__ bool wire_current(uint64_t w, uint64_t header) {
-  return (w >> 50) == (header >> 50);
-}
 // Payload of a composite (make_comp order); 0 stays 0.
 __device__ __forceinline__ uint64_t wire_payload(uint64_t comp) {
   if (comp == 0ull) return 0ull;
@@ -1088,16 +1078,6 @@ __device__ __forceinline__ uint64_t comp_of_payload(uint64_t w) {
   if (w == 0ull) return 0ull;
   return make_comp(static_cast<uint32_t>(w >> kWireIdBits),
                    kWireVocab - 1u - static_cast<uint32_t>(w & (kWireVocab - 1u)));
-}
-// Greedy composite <-> payload (high word = greedy key, low word = ~id).
-__device__ __forceinline__ uint64_t greedy_payload(uint64_t g) {
-  if (g == 0ull) return 0ull;
-  return ((g >> 32) << kWireIdBits) | static_cast<uint64_t>(kWireVocab - 1u - greedy_id(g));
-}
-__device__ __forceinline__ uint64_t greedy_of_payload(uint64_t w) {
-  if (w == 0ull) return 0ull;
-  const uint32_t id = kWireVocab - 1u - static_cast<uint32_t>(w & (kWireVocab - 1u));
-  return ((w >> kWireIdBits) << 32) | static_cast<uint64_t>(~id);
 }
 
 // c + 1 when chunk c finishes each row (finisher hand-off), else 0.

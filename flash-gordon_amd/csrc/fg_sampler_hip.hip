@@ -672,6 +672,11 @@ struct fg_hip_output_slice {
   uint32_t vocab, ways, first_row, rows, max_batch;
   unsigned long long* d_keys;  // per batch row; zero between calls
   uint32_t* d_arrivals;        // per batch row; zero between calls
+  // Tagged hand-off (fg::slice_owner_kernel): words [batch row][chunk] and
+  // per-row epochs; the wait limit in s_memrealtime ticks.
+  uint64_t* d_words;
+  uint32_t* d_epochs;
+  uint32_t wait_ticks;
   // Sampled LM-head workspace (fg::LmSampleArgs), for whole-head slices.
   uint32_t wg_cap, grp_cap;
   uint64_t* d_wg_lists;
@@ -704,6 +709,16 @@ fg_status fg_hip_output_slice_create(fg_hip_output_slice** out, uint32_t vocab, 
   if (e == hipSuccess) e = hipMalloc(&s->d_arrivals, sizeof(uint32_t) * max_batch_rows);
   if (e == hipSuccess) e = hipMemset(s->d_keys, 0, sizeof(unsigned long long) * max_batch_rows);
   if (e == hipSuccess) e = hipMemset(s->d_arrivals, 0, sizeof(uint32_t) * max_batch_rows);
+  {
+    const size_t chunks = (rows + fg::kSliceChunk - 1u) / fg::kSliceChunk;
+    const size_t words = sizeof(uint64_t) * chunks * max_batch_rows;
+    if (e == hipSuccess) e = hipMalloc(&s->d_words, words);
+    if (e == hipSuccess) e = hipMalloc(&s->d_epochs, sizeof(uint32_t) * max_batch_rows);
+    if (e == hipSuccess) e = hipMemset(s->d_words, 0, words);
+    if (e == hipSuccess) e = hipMemset(s->d_epochs, 0, sizeof(uint32_t) * max_batch_rows);
+    s->wait_ticks = static_cast<uint32_t>(
+        std::min<uint64_t>(UINT32_MAX, tuning_from_env().wait_us * 100u));
+  }
   if (ways == 1u) {
     // Two tokens per pass: lists of every workgroup and every group.
     s->wg_cap = dense_groups(rows);
@@ -750,6 +765,8 @@ void fg_hip_output_slice_destroy(fg_hip_output_slice* s) {
   if (!s) return;
   (void)hipFree(s->d_keys);
   (void)hipFree(s->d_arrivals);
+  (void)hipFree(s->d_words);
+  (void)hipFree(s->d_epochs);
   (void)hipFree(s->d_wg_lists);
   (void)hipFree(s->d_wg_count);
   (void)hipFree(s->d_lm_lines);
@@ -761,6 +778,81 @@ void fg_hip_output_slice_destroy(fg_hip_output_slice* s) {
 
 uint32_t fg_hip_output_slice_ways(const fg_hip_output_slice* s) { return s ? s->ways : 0u; }
 
+namespace {
+
+// Whether every workgroup of a slice step's grid can be resident at once
+// (the tagged hand-off's chunk 0 waits for the row's other chunks).
+bool slice_grid_resident(uint32_t groups) {
+  static std::atomic<int> occ{0};
+  int per_cu = occ.load(std::memory_order_relaxed);
+  if (!per_cu) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&fg::slice_owner_kernel<true>), fg::kSliceBlock,
+            0) != hipSuccess || per_cu <= 0)
+      return false;
+    occ.store(per_cu, std::memory_order_relaxed);
+  }
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return false;
+  return static_cast<uint64_t>(groups) <= static_cast<uint64_t>(per_cu) * static_cast<uint64_t>(cus);
+}
+
+// The ways' spans checked (they tile [0, vocab)) into `spans`.
+bool split_spans(uint32_t ways, uint32_t vocab, const uint32_t* span_first,
+                 const uint32_t* span_rows, fg::SplitSpans* spans) {
+  static const uint32_t kRanks[fg::kSplitWaysMax] = {4u, 0u, 1u, 2u};
+  uint64_t cursor = 0;
+  for (uint32_t w = 0; w < ways; w++) {
+    if (span_first[w] != cursor || !span_rows[w]) return false;
+    cursor += span_rows[w];
+    spans->first[w] = span_first[w];
+    spans->rows[w] = span_rows[w];
+    spans->rank[w] = kRanks[w];
+  }
+  return cursor == vocab;
+}
+
+// One owner step over the slice: the tagged hand-off when the slice's ids fit
+// a word and its grid is resident at once, else one workgroup a row.
+hipError_t slice_step(fg_hip_output_slice* s, const float* logits, uint64_t stride,
+                      uint32_t batch_rows, float* values, uint32_t* ids, int32_t* row_status,
+                      fg::SliceOwner o, hipStream_t stream) {
+  const dim3 grid((s->rows + fg::kSliceChunk - 1u) / fg::kSliceChunk, batch_rows);
+  const bool vec = aligned16(logits) && stride % 4u == 0u && s->rows % 4u == 0u;
+  const bool tagged = static_cast<uint64_t>(s->first_row) + s->rows <= fg::kWireVocab &&
+                      grid.x <= static_cast<uint32_t>(fg::kWave) &&
+                      slice_grid_resident(grid.x * grid.y);
+  if (tagged) {
+    o.words = s->d_words;
+    o.epochs = s->d_epochs;
+    o.wait_ticks = s->wait_ticks;
+    if (vec)
+      fg::slice_owner_kernel<true><<<grid, fg::kSliceBlock, 0, stream>>>(
+          values, ids, row_status, logits, stride, s->first_row, s->rows, o);
+    else
+      fg::slice_owner_kernel<false><<<grid, fg::kSliceBlock, 0, stream>>>(
+          values, ids, row_status, logits, stride, s->first_row, s->rows, o);
+  } else if (vec) {
+    fg::slice_row_kernel<true><<<batch_rows, fg::kRowBlock, 0, stream>>>(
+        values, ids, row_status, logits, stride, s->first_row, s->rows, o);
+  } else {
+    fg::slice_row_kernel<false><<<batch_rows, fg::kRowBlock, 0, stream>>>(
+        values, ids, row_status, logits, stride, s->first_row, s->rows, o);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+fg_status fg_hip_output_slice_set_wait_limit(fg_hip_output_slice* s, uint64_t wait_us,
+                                             fg_error* err) {
+  if (!s || wait_us > 42000000u) return arg_fail(err, "invalid output slice wait limit");
+  s->wait_ticks = static_cast<uint32_t>(wait_us * 100u);
+  return FG_OK;
+}
+
 fg_status fg_hip_output_slice_reduce(fg_hip_output_slice* s, const float* logits,
                                      uint64_t stride, uint32_t batch_rows, float* values,
                                      uint32_t* ids, int32_t* row_status, void* stream,
@@ -768,17 +860,33 @@ fg_status fg_hip_output_slice_reduce(fg_hip_output_slice* s, const float* logits
   if (!s || !logits || !values || !ids || !row_status || !batch_rows ||
       batch_rows > s->max_batch || stride < s->rows)
     return arg_fail(err, "invalid output slice run arguments");
-  const dim3 grid((s->rows + fg::kSliceChunk - 1u) / fg::kSliceChunk, batch_rows);
-  if (aligned16(logits) && stride % 4u == 0u && s->rows % 4u == 0u)
-    fg::slice_finalist_kernel<true><<<grid, fg::kSliceBlock, 0, as_stream(stream)>>>(
-        values, ids, row_status, logits, stride, s->first_row, s->rows, s->d_keys,
-        s->d_arrivals);
-  else
-    fg::slice_finalist_kernel<false><<<grid, fg::kSliceBlock, 0, as_stream(stream)>>>(
-        values, ids, row_status, logits, stride, s->first_row, s->rows, s->d_keys,
-        s->d_arrivals);
-  const hipError_t e = hipGetLastError();
+  const hipError_t e = slice_step(s, logits, stride, batch_rows, values, ids, row_status,
+                                  fg::SliceOwner{}, as_stream(stream));
   return e == hipSuccess ? FG_OK : hip_fail(err, e, "output slice launch");
+}
+
+fg_status fg_hip_output_slice_reduce_combine(
+    fg_hip_output_slice* s, const float* logits, uint64_t stride, uint32_t batch_rows,
+    const float* part_values, const uint32_t* part_ids, const uint8_t* part_ranks,
+    const uint32_t* span_first, const uint32_t* span_rows, uint32_t* tokens, float* logits_out,
+    int32_t* row_status, void* stream, fg_error* err) {
+  fg::SliceOwner o{};
+  if (!s || !logits || !part_values || !part_ids || !part_ranks || !span_first || !span_rows ||
+      !tokens || !row_status || !batch_rows || batch_rows > s->max_batch || stride < s->rows ||
+      (s->ways != 2u && s->ways != 4u) ||
+      !split_spans(s->ways, s->vocab, span_first, span_rows, &o.spans))
+    return arg_fail(err, "invalid output slice step arguments");
+  o.combine = 1u;
+  o.ways = s->ways;
+  o.vocab = s->vocab;
+  o.part_values = part_values;
+  o.part_ids = part_ids;
+  o.part_ranks = part_ranks;
+  o.tokens = tokens;
+  o.logits_out = logits_out;
+  const hipError_t e = slice_step(s, logits, stride, batch_rows, nullptr, nullptr, row_status,
+                                  o, as_stream(stream));
+  return e == hipSuccess ? FG_OK : hip_fail(err, e, "output slice step launch");
 }
 
 // ---- Q8_0 cooked matrix-vector products ------------------------------------
@@ -880,18 +988,9 @@ fg_status fg_hip_output_split_combine(uint32_t* tokens, float* logits_out, int32
   if (!tokens || !row_status || !part_values || !part_ids || !part_ranks || !rows ||
       (ways != 2u && ways != 4u) || !vocab || !span_first || !span_rows)
     return arg_fail(err, "invalid output split combine arguments");
-  static const uint32_t kRanks[fg::kSplitWaysMax] = {4u, 0u, 1u, 2u};
   fg::SplitSpans spans{};
-  uint64_t cursor = 0;
-  for (uint32_t w = 0; w < ways; w++) {
-    if (span_first[w] != cursor || !span_rows[w])
-      return arg_fail(err, "invalid output split combine arguments");
-    cursor += span_rows[w];
-    spans.first[w] = span_first[w];
-    spans.rows[w] = span_rows[w];
-    spans.rank[w] = kRanks[w];
-  }
-  if (cursor != vocab) return arg_fail(err, "invalid output split combine arguments");
+  if (!split_spans(ways, vocab, span_first, span_rows, &spans))
+    return arg_fail(err, "invalid output split combine arguments");
   fg::split_combine_kernel<<<(rows + 255u) / 256u, 256, 0, as_stream(stream)>>>(
       tokens, logits_out, row_status, part_values, part_ids, part_ranks, rows, ways, vocab,
       spans);

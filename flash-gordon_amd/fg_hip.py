@@ -47,6 +47,7 @@ EXPORTS = (
     "fg_output_split_rank", "fg_output_split_span", "fg_output_split_combine_finalists",
     "fg_hip_output_slice_create", "fg_hip_output_slice_destroy", "fg_hip_output_slice_ways",
     "fg_hip_output_slice_reduce", "fg_hip_output_split_combine",
+    "fg_hip_output_slice_reduce_combine", "fg_hip_output_slice_set_wait_limit",
     "fg_f16_to_f32", "fg_f32_to_f16", "fg_quantize_q8_0", "fg_dequantize_q8_0",
     "fg_q8_0_cooked_tile_bytes", "fg_q8_0_cooked_matrix_bytes", "fg_cook_q8_0_rows",
     "fg_uncook_q8_0_rows", "fg_hip_dense_q8_0_cooked", "fg_hip_output_slice_run_dense",
@@ -175,6 +176,9 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "fg_hip_output_slice_destroy": (None, [P]),
         "fg_hip_output_slice_ways": (u32, [P]),
         "fg_hip_output_slice_reduce": (C.c_int, [P, P, u64, u32, P, P, P, P, E]),
+        "fg_hip_output_slice_reduce_combine":
+            (C.c_int, [P, P, u64, u32, P, P, P, P, P, P, P, P, P, E]),
+        "fg_hip_output_slice_set_wait_limit": (C.c_int, [P, u64, E]),
         "fg_hip_output_split_combine":
             (C.c_int, [P, P, P, P, P, P, u32, u32, u32, P, P, P, E]),
         "fg_f16_to_f32": (f32, [C.c_uint16]),
@@ -460,6 +464,26 @@ class OutputSlice:
         _check(self._lib.fg_hip_output_slice_reduce(
             self.handle, _ptr(logits), stride, batch_rows, _ptr(values), _ptr(ids),
             _ptr(row_status), _stream(stream), C.byref(err)), err)
+
+    def reduce_combine(self, logits, part_values, part_ids, part_ranks, spans, tokens,
+                       logits_out, row_status, batch_rows=None, stride=None, stream=None):
+        """fg_hip_output_slice_reduce_combine: the owner's step in one launch;
+        spans = [(first, rows)] by way."""
+        batch_rows = batch_rows if batch_rows is not None else logits.shape[0]
+        stride = stride if stride is not None else logits.stride(0)
+        first = (C.c_uint32 * len(spans))(*[f for f, _ in spans])
+        count = (C.c_uint32 * len(spans))(*[r for _, r in spans])
+        err = FgError()
+        _check(self._lib.fg_hip_output_slice_reduce_combine(
+            self.handle, _ptr(logits), stride, batch_rows, _ptr(part_values), _ptr(part_ids),
+            _ptr(part_ranks), first, count, _ptr(tokens), _ptr(logits_out), _ptr(row_status),
+            _stream(stream), C.byref(err)), err)
+
+    def set_wait_limit(self, wait_us):
+        """fg_hip_output_slice_set_wait_limit."""
+        err = FgError()
+        _check(self._lib.fg_hip_output_slice_set_wait_limit(self.handle, wait_us, C.byref(err)),
+               err)
 
 
 # ---- batched sampler -------------------------------------------------------

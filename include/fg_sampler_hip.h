@@ -320,12 +320,40 @@ uint32_t fg_hip_output_slice_ways(const fg_hip_output_slice *slice);
  * vocabulary id first_row + i.  values[r], ids[r] receive the row's best
  * (value, id) in fg_output_better's order; row_status[r] is FG_OK, or
  * FG_ERR_MISMATCH when that value is non-finite ("invalid output slice
- * finalist").  One launch; calls on one slice must not overlap (they share
- * its workspace). */
+ * finalist"), or FG_ERR_UNAVAILABLE (value -inf, id 0xffffffff) when the
+ * step's tagged hand-off waited past the slice's wait limit (see
+ * fg_hip_output_slice_reduce_combine).  One launch; calls on one slice must
+ * not overlap (they share its workspace). */
 fg_status fg_hip_output_slice_reduce(fg_hip_output_slice *slice, const float *logits,
                                      uint64_t stride, uint32_t batch_rows, float *values,
                                      uint32_t *ids, int32_t *row_status, void *stream,
                                      fg_error *err);
+
+/* fg_hip_output_slice_reduce and fg_hip_output_split_combine in one launch:
+ * the owner's step of src/runtime.c:2440-2466 (its own slice reduced, then
+ * combined with the finalists the other ranks sent) for a slice of 2 or 4
+ * ways.  part_*[r*ways + i] for i >= 1 and span_first/span_rows are as for
+ * fg_hip_output_split_combine (part_*[r*ways + 0] is not read: the own
+ * finalist is computed here); tokens/logits_out (may be NULL)/row_status as
+ * there.  No counterpart entry point in the reference, whose owner runs the
+ * two halves back to back.  When the step's grid fits the device at once
+ * and the slice's ids are below 2^18, the slice's chunks hand their bests to
+ * the row's last chunk through tagged words; otherwise one workgroup streams
+ * each row.  A row whose finishing chunk waited past the slice's wait limit
+ * gets status FG_ERR_UNAVAILABLE and token 0xffffffff.  Replays of a
+ * captured launch are exact: the words' epochs live on the device. */
+fg_status fg_hip_output_slice_reduce_combine(
+    fg_hip_output_slice *slice, const float *logits, uint64_t stride, uint32_t batch_rows,
+    const float *part_values, const uint32_t *part_ids, const uint8_t *part_ranks,
+    const uint32_t *span_first, const uint32_t *span_rows, uint32_t *tokens, float *logits_out,
+    int32_t *row_status, void *stream, fg_error *err);
+
+/* The tagged hand-off's wait limit for the slice's steps, in microseconds
+ * (initially FG_HIP_FINISHER_WAIT_US or 100,000; at most 42,000,000; 0 gives
+ * up at the first poll that finds a word missing).  No counterpart in the
+ * reference. */
+fg_status fg_hip_output_slice_set_wait_limit(fg_hip_output_slice *slice, uint64_t wait_us,
+                                             fg_error *err);
 
 /* fg_output_slice_run_hidden (src/output.c:367-383): its dense product
  * (output_slice_reduce, src/output.c:320-344) fused with its reduction: weights are the slice's cooked rows

@@ -193,3 +193,184 @@ def test_split_combine_arguments(dev):
         fg_hip.split_combine(z, None, z, z, z, z, 2, 2, 100, [(0, 50), (50, 49)])
     with pytest.raises(fg_hip.FgStatusError):
         fg_hip.split_combine(z, None, z, z, z, z, 2, 3, 99, [(0, 33), (33, 33), (66, 33)])
+
+
+def _parts(rng, rows, ways, vocab, spans, bad=True):
+    """Finalists the other ranks sent (way i >= 1 at column i), some bad."""
+    vals = rng.normal(0, 2, (rows, ways)).astype(np.float32)
+    ids = np.zeros((rows, ways), dtype=np.uint32)
+    ranks = np.zeros((rows, ways), dtype=np.uint8)
+    for r in range(rows):
+        order = rng.permutation(ways - 1) + 1
+        for j, w in enumerate(order, start=1):
+            ranks[r, j] = (4, 0, 1, 2)[w]
+            first, n = spans[w]
+            ids[r, j] = first + rng.integers(0, n)
+        if bad:
+            kind = r % 8
+            if kind == 1:
+                ranks[r, 1] = 3  # owns no slice
+            elif kind == 2:
+                vals[r, 1] = 60.0  # beats the owner's slice
+            elif kind == 3:
+                vals[r, ways - 1] = np.nan
+            elif kind == 4:
+                ids[r, 1] = vocab + 2
+    return vals, ids, ranks
+
+
+def _step(dev, sl, x, vals, ids, ranks, spans, stride=None):
+    import torch
+    rows = x.shape[0]
+    tx = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    tv = torch.from_numpy(vals).to(dev)
+    ti = torch.from_numpy(ids.view(np.int32)).to(dev)
+    tr = torch.from_numpy(ranks).to(dev)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    lg = torch.empty(rows, dtype=torch.float32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    sl.reduce_combine(tx, tv, ti, tr, spans, tok, lg, st)
+    torch.cuda.synchronize()
+    return u32(tok), lg.cpu().numpy(), st.cpu().numpy()
+
+
+def _step_two_launches(dev, sl, x, vals, ids, ranks, ways, vocab, spans):
+    own_v, own_i, _ = _slice_reduce(dev, sl, x)
+    v, i = vals.copy(), ids.copy()
+    v[:, 0], i[:, 0] = own_v, own_i
+    return _combine(dev, v, i, ranks, ways, vocab, spans)
+
+
+@pytest.mark.parametrize("ways,rows", [(4, 64), (2, 64), (4, 5)])
+def test_slice_step_matches_reduce_then_combine(dev, ways, rows):
+    """fg_hip_output_slice_reduce_combine (one launch, tagged hand-off to
+    chunk 0, combine in the same workgroup) against the two entry points it
+    fuses, and against the oracle's combine of the oracle's finalist; three
+    calls on one slice with new inputs each."""
+    spans = [fg_hip.split_span(ways, w) for w in range(ways)]
+    first, n = spans[0]
+    sl = fg_hip.OutputSlice(Q38, ways, first, n, 64)
+    for call in range(3):
+        rng = np.random.default_rng(ways * 100 + rows + call)
+        x = _rows(rng, rows, n)
+        vals, ids, ranks = _parts(rng, rows, ways, Q38, spans)
+        got = _step(dev, sl, x, vals, ids, ranks, spans)
+        want = _step_two_launches(dev, sl, x, vals, ids, ranks, ways, Q38, spans)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[2], want[2])
+        ok = want[2] == 0
+        assert np.array_equal(got[1][ok].view(np.uint32), want[1][ok].view(np.uint32))
+        ov, oi, _ = O.slice_finalists(x, first)
+        for r in range(rows):
+            v, i = vals[r].copy(), ids[r].copy()
+            v[0], i[0] = ov[r], oi[r]
+            ws, wt, _ = O.split_combine_row(v, i, ranks[r], ways, Q38, spans)
+            assert got[2][r] == ws and got[0][r] == wt, (call, r)
+
+
+def test_slice_step_graph_replays(dev):
+    """A captured step replayed over new inputs written between replays:
+    every replay exact (the hand-off's epochs advance on the device)."""
+    import torch
+    ways, rows = 4, 64
+    spans = [fg_hip.split_span(ways, w) for w in range(ways)]
+    first, n = spans[0]
+    sl = fg_hip.OutputSlice(Q38, ways, first, n, rows)
+    tx = torch.zeros(rows, n, device=dev)
+    tv = torch.zeros(rows, ways, device=dev)
+    ti = torch.zeros(rows, ways, dtype=torch.int32, device=dev)
+    tr = torch.zeros(rows, ways, dtype=torch.uint8, device=dev)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    lg = torch.empty(rows, dtype=torch.float32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        sl.reduce_combine(tx, tv, ti, tr, spans, tok, lg, st, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        sl.reduce_combine(tx, tv, ti, tr, spans, tok, lg, st, stream=s.cuda_stream)
+    for rep in range(4):
+        rng = np.random.default_rng(900 + rep)
+        x = _rows(rng, rows, n)
+        vals, ids, ranks = _parts(rng, rows, ways, Q38, spans)
+        tx.copy_(torch.from_numpy(x))
+        tv.copy_(torch.from_numpy(vals))
+        ti.copy_(torch.from_numpy(ids.view(np.int32)))
+        tr.copy_(torch.from_numpy(ranks))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ov, oi, _ = O.slice_finalists(x, first)
+        got_t, got_s = u32(tok), st.cpu().numpy()
+        for r in range(rows):
+            v, i = vals[r].copy(), ids[r].copy()
+            v[0], i[0] = ov[r], oi[r]
+            ws, wt, _ = O.split_combine_row(v, i, ranks[r], ways, Q38, spans)
+            assert got_s[r] == ws and got_t[r] == wt, (rep, r)
+
+
+def test_slice_wait_limit_reports_and_next_call_is_exact(dev):
+    """A wait limit of 0: chunk 0 gives up on any word not yet there (status
+    FG_ERR_UNAVAILABLE, token 0xffffffff) or finishes exactly; the next call,
+    with the limit back, is exact."""
+    ways, rows = 4, 64
+    spans = [fg_hip.split_span(ways, w) for w in range(ways)]
+    first, n = spans[0]
+    sl = fg_hip.OutputSlice(Q38, ways, first, n, rows)
+    rng = np.random.default_rng(31)
+    x = _rows(rng, rows, n)
+    vals, ids, ranks = _parts(rng, rows, ways, Q38, spans, bad=False)
+    want = _step_two_launches(dev, sl, x, vals, ids, ranks, ways, Q38, spans)
+    sl.set_wait_limit(0)
+    tok, _, st = _step(dev, sl, x, vals, ids, ranks, spans)
+    gave_up = st == 7
+    assert np.all(tok[gave_up] == 0xFFFFFFFF)
+    assert np.array_equal(tok[~gave_up], want[0][~gave_up])
+    sl.set_wait_limit(100_000)
+    tok, _, st = _step(dev, sl, x, vals, ids, ranks, spans)
+    assert np.array_equal(tok, want[0]) and np.array_equal(st, want[2])
+
+
+def test_slice_step_one_workgroup_a_row(dev):
+    """Steps the tagged hand-off does not take (a batch whose grid is not
+    resident at once; a slice whose ids reach 2^18): one workgroup a row,
+    against the oracle, for the reduction and the fused step."""
+    import torch
+    ways, rows = 4, 640  # 5 chunks x 640 rows: more workgroups than fit at once
+    spans = [fg_hip.split_span(ways, w) for w in range(ways)]
+    first, n = spans[0]
+    sl = fg_hip.OutputSlice(Q38, ways, first, n, rows)
+    rng = np.random.default_rng(61)
+    x = _rows(rng, rows, n)
+    vals, ids, ranks = _parts(rng, rows, ways, Q38, spans)
+    tok, _, st = _step(dev, sl, x, vals, ids, ranks, spans)
+    ov, oi, os_ = O.slice_finalists(x, first)
+    for r in range(rows):
+        v, i = vals[r].copy(), ids[r].copy()
+        v[0], i[0] = ov[r], oi[r]
+        ws, wt, _ = O.split_combine_row(v, i, ranks[r], ways, Q38, spans)
+        assert st[r] == ws and tok[r] == wt, r
+    _check(_slice_reduce(dev, sl, x), (ov, oi, os_))
+    big, first2 = 400_000, 200_000  # ids up to 399,998
+    for n2 in (199_996, 199_999):  # float4 loads; an odd slice: scalar loads
+        sl2 = fg_hip.OutputSlice(big, 2, first2, n2, 8)
+        y = _rows(rng, 8, n2)
+        _check(_slice_reduce(dev, sl2, y), O.slice_finalists(y, first2))
+
+
+def test_slice_step_arguments(dev):
+    import torch
+    spans = [fg_hip.split_span(4, w) for w in range(4)]
+    first, n = spans[0]
+    sl = fg_hip.OutputSlice(Q38, 4, first, n, 8)
+    x = torch.zeros(8, n, device=dev)
+    z = torch.zeros(32, dtype=torch.int32, device=dev)
+    with pytest.raises(fg_hip.FgStatusError):  # spans do not tile the vocabulary
+        sl.reduce_combine(x, z, z, z, spans[:3], z, None, z)
+    with pytest.raises(fg_hip.FgStatusError):  # more rows than max_batch_rows
+        sl.reduce_combine(x, z, z, z, spans, z, None, z, batch_rows=9)
+    with pytest.raises(fg_hip.FgStatusError):
+        sl.set_wait_limit(10**9)
+    whole = fg_hip.OutputSlice(Q38, 1, 0, Q38, 8)  # one way: nothing to combine
+    with pytest.raises(fg_hip.FgStatusError):
+        whole.reduce_combine(torch.zeros(8, Q38, device=dev), z, z, z, [(0, Q38)], z, None, z)
