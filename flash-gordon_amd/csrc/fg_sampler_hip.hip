@@ -476,13 +476,20 @@ fg_status sample_launch(const Workspace& w, const RowParams* h_params, uint32_t 
   {
     // Finisher protocol (see the kernel): every row a top list of at most 64
     // (no greedy row, no log-probs) over 2-8 chunks, or every row greedy (no
-    // log-probs) over 2-64 chunks; ids that fit a tagged word.
-    bool ok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= 8u && b->logprobs == 0u &&
-              vocab <= fg::kWireVocab;
+    // log-probs) over 2-64 chunks; ids that fit a tagged word.  Not for a
+    // launch being captured into a graph: its replays would all carry the
+    // epoch it was captured with, so a word left by the previous replay
+    // would pass for the current one; the last-arriver hand-off keeps no
+    // state between launches.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess) capture = hipStreamCaptureStatusNone;
+    const bool eager = capture == hipStreamCaptureStatusNone;
+    bool ok = eager && w.tuning.finisher != 0 && chunks >= 2u && chunks <= 8u &&
+              b->logprobs == 0u && vocab <= fg::kWireVocab;
     for (uint32_t r = 0; ok && r < b->rows; r++)
       ok = h_params[r].temperature > 0.0f && h_params[r].top_k >= 1u &&
            h_params[r].top_k <= static_cast<uint32_t>(fg::kMaxK);
-    bool gok = w.tuning.finisher != 0 && chunks >= 2u && chunks <= fg::kMaxChunks &&
+    bool gok = eager && w.tuning.finisher != 0 && chunks >= 2u && chunks <= fg::kMaxChunks &&
                b->logprobs == 0u && vocab <= fg::kWireVocab;
     for (uint32_t r = 0; gok && r < b->rows; r++) gok = h_params[r].temperature == 0.0f;
     ok = ok || gok;

@@ -867,12 +867,15 @@ constexpr uint64_t kReduceAllSlotOffset =
     kReduceAllListOffset + uint64_t{kReduceAllList} * (sizeof(uint64_t) + sizeof(uint32_t));
 static_assert(sizeof(ReduceAllWork) <= kReduceAllHeader, "header");
 static_assert(kReduceAllSlotOffset % 8u == 0u, "slot alignment");
-// Bytes of the workspace for `tiles` tiles: the fixed part, then per tile a
-// bound (8 B), a slot (8 B: tag << 32 | count) and a region of composites
-// and score bits.
+// Bytes of the workspace for `tiles` tiles: the fixed part (with a bound
+// (8 B) and a slot (8 B: tag << 32 | count) for each of kReduceAllMaxTiles
+// tiles, at the same addresses for every tile count, so a slot word left by
+// an earlier call always carries an older tag), then per tile a region of
+// composites and score bits.
+constexpr uint64_t kReduceAllRegionOffset =
+    kReduceAllSlotOffset + uint64_t{kReduceAllMaxTiles} * 2u * sizeof(uint64_t);
 __host__ __device__ constexpr uint64_t reduce_all_bytes(uint64_t tiles) {
-  return kReduceAllSlotOffset + tiles * 2u * sizeof(uint64_t) +
-         tiles * kReduceAllRegion * (sizeof(uint64_t) + sizeof(uint32_t));
+  return kReduceAllRegionOffset + tiles * kReduceAllRegion * (sizeof(uint64_t) + sizeof(uint32_t));
 }
 
 // Sense-reversing grid barrier: the last workgroup in (its arrival number
@@ -993,8 +996,8 @@ __global__ __launch_bounds__(kReduceBlock) void topk_reduce_all_kernel(
   uint64_t* const list_comp = reinterpret_cast<uint64_t*>(work_bytes + kReduceAllListOffset);
   uint32_t* const list_bits = reinterpret_cast<uint32_t*>(list_comp + kReduceAllList);
   uint64_t* const slot_bound = reinterpret_cast<uint64_t*>(work_bytes + kReduceAllSlotOffset);
-  uint64_t* const slot_tag = slot_bound + tiles;
-  uint64_t* const region_comp = slot_tag + tiles;
+  uint64_t* const slot_tag = slot_bound + kReduceAllMaxTiles;
+  uint64_t* const region_comp = reinterpret_cast<uint64_t*>(work_bytes + kReduceAllRegionOffset);
   uint32_t* const region_bits = reinterpret_cast<uint32_t*>(region_comp + uint64_t{tiles} * kReduceAllRegion);
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & (kWave - 1u);

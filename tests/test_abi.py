@@ -52,13 +52,12 @@ def test_argument_errors_without_device_work():
 
 
 def test_reduce_all_workspace_bytes():
-    """Fixed part (header, six 4096-bucket tables, a 6144-entry list), then per
-    4096-score tile an 8-byte bound, an 8-byte slot and a 1024-entry region of
-    12-byte entries."""
-    fixed = 64 + 6 * 4096 * 4 + 6144 * 12
+    """Fixed part (header, six 4096-bucket tables, a 6144-entry list, a bound
+    and a slot of 8 bytes each for 1,024 tiles), then per 4096-score tile a
+    1024-entry region of 12-byte entries."""
+    fixed = 64 + 6 * 4096 * 4 + 6144 * 12 + 1024 * 16
     for count, tiles in ((1, 1), (4096, 1), (4097, 2), (262_144, 64), (300_000, 74)):
-        want = fixed + tiles * 16 + tiles * 1024 * 12
-        assert fg_hip.topk_reduce_all_workspace_bytes(count) == want
+        assert fg_hip.topk_reduce_all_workspace_bytes(count) == fixed + tiles * 1024 * 12
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -713,6 +713,53 @@ def test_graph_replays_match_eager(dev, nucleus):
         assert np.array_equal(st.cpu().numpy(), eager["status"]), replay
 
 
+@pytest.mark.parametrize("greedy", [False, True])
+def test_graph_replays_over_new_inputs(dev, greedy):
+    """One captured sample call replayed four times in a row, new logits,
+    counts and uniforms written into the captured buffers before each
+    replay: every replay matches the oracle on its own inputs (a replay
+    must not take a word the previous replay left)."""
+    import torch
+    rows = 16
+    s = fg_hip.HipSampler(W.V, rows)
+    base = W.config2(rows=rows)
+    if greedy:
+        for c in base["configs"]:
+            c["temperature"] = 0.0
+    s.set_configs([fg_hip.make_config(c["temperature"], c["top_p"], c["top_k"], c["presence"],
+                                      c["frequency"], c["repetition"]) for c in base["configs"]])
+    d_logits = to_dev(base["logits"], dev)
+    d_counts = to_dev(base["counts"], dev)
+    d_u = to_dev(base["uniforms"], dev)
+    tok = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+    st = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            s.sample(d_logits, d_u, tok, counts=d_counts, row_status=st, stream=side.cuda_stream)
+    torch.cuda.synchronize()
+    for replay in range(4):
+        rng = np.random.default_rng(500 + replay)
+        w = dict(base)
+        w["logits"] = rng.normal(0, 2, base["logits"].shape).astype(np.float32)
+        w["counts"] = rng.integers(0, 3, base["counts"].shape).astype(np.uint32) * \
+            (rng.random(base["counts"].shape) < 0.01)
+        w["uniforms"] = rng.random(rows).astype(np.float32)
+        d_logits.copy_(torch.from_numpy(w["logits"]))
+        d_counts.copy_(torch.from_numpy(w["counts"].astype(np.uint32).view(np.int32)))
+        d_u.copy_(torch.from_numpy(w["uniforms"]))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = W.oracle_run(w)
+        got = tok.cpu().numpy().view(np.uint32)
+        assert np.array_equal(st.cpu().numpy(), ref["status"]), replay
+        ok = (got == ref["token"]) | (ref["margin"] < BOUNDARY)
+        assert ok.all(), (replay, got, ref["token"])
+
+
 def test_prepared_launch_matches_sample(dev):
     """HipSampler.prepare (the batch marshalled once, launched per call)
     gives the oracle's tokens, call after call on the same buffers."""
