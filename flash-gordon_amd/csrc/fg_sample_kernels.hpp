@@ -1163,17 +1163,26 @@ __device__ __forceinline__ void rank_place64(const uint64_t* lists, uint32_t str
   if (e != 0ull && r < kk) out[r] = e;
 }
 
-// The finisher's eight lists in LDS.  Lists of at most 32 (list c at
-// lists32 + 32 c): lanes 0-31 of wave w place the entries of list 2w, lanes
-// 32-63 those of list 2w + 1.  Longer lists (list c at lists64 + 64 c): wave
-// w places both lists' entries, a position per lane.
+// The finisher's eight lists in LDS (lists past the row's chunk count
+// empty, so with at most 4 chunks only lists 0-3 are searched).  Lists of at
+// most 32 (list c at lists32 + 32 c): lanes 0-31 of wave w place the entries
+// of list 2w, lanes 32-63 those of list 2w + 1.  Longer lists (list c at
+// lists64 + 64 c): with at most 4 chunks wave w places list w's entries, a
+// position per lane; else both of lists 2w and 2w + 1.
 __device__ __forceinline__ void rank_place_lists(const uint64_t* lists32, const uint64_t* lists64,
-                                                 uint32_t wave, uint32_t kk, uint64_t* out) {
+                                                 uint32_t wave, uint32_t kk, uint32_t chunks,
+                                                 uint64_t* out) {
   const uint32_t lane = lane_id();
   if (kk <= 32u) {
     const uint32_t c = 2u * wave + (lane >= 32u ? 1u : 0u);
     const uint32_t pos = lane & 31u;
-    rank_place<8>(lists32, 32u, pos < kk ? lists32[c * 32u + pos] : 0ull, kk, out);
+    const uint64_t e = pos < kk ? lists32[c * 32u + pos] : 0ull;
+    if (chunks <= 4u)
+      rank_place<4>(lists32, 32u, e, kk, out);
+    else
+      rank_place<8>(lists32, 32u, e, kk, out);
+  } else if (chunks <= 4u) {
+    rank_place64<4>(lists64, 64u, lane < kk ? lists64[wave * 64u + lane] : 0ull, kk, out);
   } else {
 #pragma unroll
     for (uint32_t h = 0; h < 2u; h++) {
@@ -1406,11 +1415,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
     }
     __syncthreads();
     // (Nucleus rows keep top lists, so launches with them have kTop.)
-#ifndef FG_NO_DEEP_CALL
     if constexpr (F::kTop) {
-#else
-    if constexpr (false) {
-#endif
       if (__builtin_expect(s_nuc_deep != 0u, 0)) {
         static_assert(sizeof(NucLds<FusedNuc>) <= sizeof(s_buf), "deep-row LDS");
         // Everything the descent needs is re-read here, so the streaming
@@ -1431,7 +1436,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
     if (F::kTop && fin_wg) {
       // The finisher's helpers: wave 0 fills the lists, all four rank them.
       __syncthreads();
-      rank_place_lists(&s_top[0][0], &s_buf[0][0], wave, kk, s_rank);
+      rank_place_lists(&s_top[0][0], &s_buf[0][0], wave, kk, a.chunks, s_rank);
       __syncthreads();
     }
     if constexpr (F::kNuc) nuc_tail(false, 0.0f);
@@ -1561,7 +1566,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
       if (wide || lane < 32u) lists[own * stride + lane] = lane < kk ? fin : 0ull;
       s_rank[lane] = 0ull;
       __syncthreads();
-      rank_place_lists(&s_top[0][0], &s_buf[0][0], 0u, kk, s_rank);
+      rank_place_lists(&s_top[0][0], &s_buf[0][0], 0u, kk, a.chunks, s_rank);
       __syncthreads();
       fin = lane < kk ? s_rank[lane] : 0ull;
       if (spec) {
