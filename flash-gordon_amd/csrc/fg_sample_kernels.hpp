@@ -1379,10 +1379,14 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
   // one composite per chunk.
   const bool gfin_mode = F::kGreedy && finisher_of(a) != 0u && greedy && L == 0u &&
                          a.chunks >= 2u && a.chunks <= static_cast<uint32_t>(kWave);
-  // Lists of at most 32: the four waves rank their own entries.
-  const bool rank_wg = F::kTop && kk != 0u && kk <= 32u;
+  // The four waves rank their own lists' entries (five- or six-step
+  // searches): lists of at most 32, and longer ones in launches without
+  // whole-row nucleus or log-prob rows (there, one wave's bitonic merges
+  // measured faster: 69.3 against 71.1 us at config 3, 215.6 against 216.1
+  // at config 5; at config 4's top-k 50, 27.64 against 27.95).
+  const bool rank_wg = F::kTop && kk != 0u && (kk <= 32u || (!F::kNuc && !F::kLse));
   if (F::kTop) s_top[wave][lane] = mine;
-  if (F::kTop && rank_wg && wave == 0 && lane < 32u) s_rank[lane] = 0ull;
+  if (F::kTop && rank_wg && wave == 0) s_rank[lane] = 0ull;
   if (lane == 0) {
     // Only the partials some row of the launch reads.
     if (F::kGreedy) s_greedy[wave] = gbest;
@@ -1399,7 +1403,10 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
   }
   __syncthreads();
   if (F::kTop && rank_wg) {
-    rank_place<kWaves>(&s_top[0][0], kWave, mine, kk, s_rank);
+    if (kk <= 32u)
+      rank_place<kWaves>(&s_top[0][0], kWave, mine, kk, s_rank);
+    else
+      rank_place64<kWaves>(&s_top[0][0], kWave, mine, kk, s_rank);
     __syncthreads();
   }
   // Launches with whole-row nucleus rows: a workgroup's waves stay to the
@@ -1447,8 +1454,8 @@ __global__ __launch_bounds__(kBlock, 3) void sample_rows_kernel(SampleArgs a) {
   double m = -INFINITY, z = 0.0;
   Mass zs{-INFINITY, 0.0, 0.0};
   if (F::kTop && kk) {
-    if (kk <= 32u) {
-      fin = lane < 32u ? s_rank[lane] : 0ull;
+    if (rank_wg) {
+      fin = lane < kk ? s_rank[lane] : 0ull;
     } else {
       // (0,1) and (2,3) side by side, then the two results.
       uint64_t a0 = s_top[0][lane], a1 = s_top[2][lane];
