@@ -319,7 +319,7 @@ constexpr size_t kOffGreedy = align256(kOffCand + sizeof(uint64_t) * kStaticSlot
 constexpr size_t kOffSpec = align256(kOffGreedy + sizeof(uint64_t) * kStaticSlots);
 constexpr size_t kOffLse = align256(kOffSpec + sizeof(uint64_t) * kStaticSlots);
 constexpr size_t kOffZsum = align256(kOffLse + sizeof(double) * kStaticSlots * 2u);
-constexpr size_t kOffDone = align256(kOffZsum + sizeof(double) * kStaticSlots * 3u);
+constexpr size_t kOffDone = align256(kOffZsum + sizeof(double) * (kStaticSlots / fg::kWaves) * 3u);
 constexpr size_t kStaticBytes = align256(kOffDone + sizeof(uint32_t) * fg::kLineWords * kStaticMaxRows);
 static_assert(kStaticBytes == FG_SAMPLER_HIP_STATIC_BYTES, "header size out of date");
 
@@ -409,12 +409,17 @@ hipError_t fill_params(const Workspace& w, const RowParams* h, uint32_t rows, hi
 // Returns the workspace's hand-off slots to zero (when the finisher epoch
 // wraps, so that no word of an earlier launch can carry the new one).
 __global__ void __launch_bounds__(256)
-    epoch_clear_kernel(uint64_t* cand, uint64_t cand_words, uint64_t* greedy, uint64_t slots) {
+    epoch_clear_kernel(uint64_t* cand, uint64_t* greedy, uint64_t* spec, uint64_t slots) {
+  // Every region that carries tagged words: lists, greedy composites and the
+  // waves' speculative keys.
   const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < cand_words;
-       i += stride) {
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < slots * fg::kMaxK; i += stride) {
     cand[i] = 0ull;
-    if (i < slots) greedy[i] = 0ull;
+    if (i < slots) {  // greedy and spec: a word per wave slot at most
+      greedy[i] = 0ull;
+      spec[i] = 0ull;
+    }
   }
 }
 
@@ -423,7 +428,7 @@ __global__ void __launch_bounds__(256)
 hipError_t next_epoch(const Workspace& w, hipStream_t stream, uint32_t* epoch) {
   uint32_t e = *w.epoch + 1u;
   if (e > fg::kMaxEpoch) {
-    epoch_clear_kernel<<<256, 256, 0, stream>>>(w.cand, w.slots * fg::kMaxK, w.greedy, w.slots);
+    epoch_clear_kernel<<<256, 256, 0, stream>>>(w.cand, w.greedy, w.spec, w.slots);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     e = 1u;
@@ -1075,7 +1080,9 @@ fg_status fg_sampler_hip_create(fg_sampler_hip** out, uint32_t vocab, uint32_t m
   if (e == hipSuccess) e = hipMemset(s->ws.greedy, 0, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.spec, sizeof(uint64_t) * slots);
   if (e == hipSuccess) e = hipMalloc(&s->ws.lse, sizeof(double) * slots * 2);
-  if (e == hipSuccess) e = hipMalloc(&s->ws.zsum, sizeof(double) * slots * 3);
+  // (A workgroup slot each: wave slots / kWaves.)
+  if (e == hipSuccess)
+    e = hipMalloc(&s->ws.zsum, sizeof(double) * ((slots + fg::kWaves - 1) / fg::kWaves) * 3u);
   const size_t done_bytes = sizeof(uint32_t) * fg::kLineWords * max_rows;
   if (e == hipSuccess) e = hipMalloc(&s->ws.row_done, done_bytes);
   if (e == hipSuccess) e = hipMemset(s->ws.row_done, 0, done_bytes);

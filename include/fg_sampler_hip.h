@@ -240,7 +240,7 @@ fg_status fg_sampler_hip_sample(fg_sampler_hip *sampler, const fg_sampler_hip_ba
  * one GPU shares that GPU's array: calls that overlap on one GPU (different
  * streams, or another thread) race and must be serialised by the caller. */
 #define FG_SAMPLER_HIP_STATIC_MAX_ROWS 256u
-#define FG_SAMPLER_HIP_STATIC_BYTES 2949120u
+#define FG_SAMPLER_HIP_STATIC_BYTES 2856960u
 fg_status fg_sampler_hip_sample_static(uint32_t vocab, const fg_sampler_config *configs,
                                        uint32_t flags, const fg_sampler_hip_batch *batch,
                                        void *stream, fg_error *err);
