@@ -495,7 +495,8 @@ def split_bench(args, torch, fg_hip, dev, w, sets, nsets, batch_bytes):
         "roofline": {"bound": "hbm", "achieved": round(alg / per_step_s / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(alg / per_step_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "fg::slice_finalist_kernel + fg::split_combine_kernel",
+                     "kernel": "fg::slice_owner_kernel (grids resident at once) or "
+                               "fg::slice_row_kernel (the library picks)",
                      "algorithmic_bytes_per_launch": alg,
                      "launch_us": round(per_step_s * 1e6, 3)},
         "wall_s": round(wall, 3)}))

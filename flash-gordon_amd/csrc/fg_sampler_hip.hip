@@ -722,8 +722,7 @@ fg_status fg_hip_output_slice_create(fg_hip_output_slice** out, uint32_t vocab, 
   if (e == hipSuccess) e = hipMemset(s->d_keys, 0, sizeof(unsigned long long) * max_batch_rows);
   if (e == hipSuccess) e = hipMemset(s->d_arrivals, 0, sizeof(uint32_t) * max_batch_rows);
   {
-    const size_t chunks = (rows + fg::kSliceChunk - 1u) / fg::kSliceChunk;
-    const size_t words = sizeof(uint64_t) * chunks * max_batch_rows;
+    const size_t words = sizeof(uint64_t) * fg::kSliceWordStride * max_batch_rows;
     if (e == hipSuccess) e = hipMalloc(&s->d_words, words);
     if (e == hipSuccess) e = hipMalloc(&s->d_epochs, sizeof(uint32_t) * max_batch_rows);
     if (e == hipSuccess) e = hipMemset(s->d_words, 0, words);
@@ -792,16 +791,24 @@ uint32_t fg_hip_output_slice_ways(const fg_hip_output_slice* s) { return s ? s->
 
 namespace {
 
+extern "C++" {
 // Whether every workgroup of a slice step's grid can be resident at once
-// (the tagged hand-off's chunk 0 waits for the row's other chunks).
+// (the tagged hand-off's finisher waits for the row's other chunks).
+template <uint32_t kChunk>
 bool slice_grid_resident(uint32_t groups) {
   static std::atomic<int> occ{0};
   int per_cu = occ.load(std::memory_order_relaxed);
   if (!per_cu) {
+    int a = 0, b = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&fg::slice_owner_kernel<true>), fg::kSliceBlock,
-            0) != hipSuccess || per_cu <= 0)
+            &a, reinterpret_cast<const void*>(&fg::slice_owner_kernel<true, kChunk>),
+            fg::kSliceBlock, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &b, reinterpret_cast<const void*>(&fg::slice_owner_kernel<false, kChunk>),
+            fg::kSliceBlock, 0) != hipSuccess)
       return false;
+    per_cu = std::min(a, b);
+    if (per_cu <= 0) return false;
     occ.store(per_cu, std::memory_order_relaxed);
   }
   int dev = 0, cus = 0;
@@ -826,27 +833,47 @@ bool split_spans(uint32_t ways, uint32_t vocab, const uint32_t* span_first,
   return cursor == vocab;
 }
 
+// The tagged owner step with kChunk logits per workgroup, if its grid has
+// at most kSliceWordStride chunks a row and is resident at once.
+template <uint32_t kChunk>
+bool slice_owner_launch(fg_hip_output_slice* s, const float* logits, uint64_t stride,
+                        uint32_t batch_rows, float* values, uint32_t* ids, int32_t* row_status,
+                        const fg::SliceOwner& o, bool vec, hipStream_t stream) {
+  const dim3 grid((s->rows + kChunk - 1u) / kChunk, batch_rows);
+  if (grid.x > fg::kSliceWordStride || !slice_grid_resident<kChunk>(grid.x * grid.y))
+    return false;
+  if (vec)
+    fg::slice_owner_kernel<true, kChunk><<<grid, fg::kSliceBlock, 0, stream>>>(
+        values, ids, row_status, logits, stride, s->first_row, s->rows, o);
+  else
+    fg::slice_owner_kernel<false, kChunk><<<grid, fg::kSliceBlock, 0, stream>>>(
+        values, ids, row_status, logits, stride, s->first_row, s->rows, o);
+  return true;
+}
+}  // extern "C++"
+
 // One owner step over the slice: the tagged hand-off when the slice's ids fit
-// a word and its grid is resident at once, else one workgroup a row.
+// a word and a grid of 2,048-, 4,096- or 8,192-logit chunks (the smallest
+// that fits: more workgroups shorten each one's load chain) is resident at
+// once, else one workgroup a row.
 hipError_t slice_step(fg_hip_output_slice* s, const float* logits, uint64_t stride,
                       uint32_t batch_rows, float* values, uint32_t* ids, int32_t* row_status,
                       fg::SliceOwner o, hipStream_t stream) {
-  const dim3 grid((s->rows + fg::kSliceChunk - 1u) / fg::kSliceChunk, batch_rows);
   const bool vec = aligned16(logits) && stride % 4u == 0u && s->rows % 4u == 0u;
-  const bool tagged = static_cast<uint64_t>(s->first_row) + s->rows <= fg::kWireVocab &&
-                      grid.x <= static_cast<uint32_t>(fg::kWave) &&
-                      slice_grid_resident(grid.x * grid.y);
-  if (tagged) {
+  bool launched = false;
+  if (static_cast<uint64_t>(s->first_row) + s->rows <= fg::kWireVocab) {
     o.words = s->d_words;
     o.epochs = s->d_epochs;
     o.wait_ticks = s->wait_ticks;
-    if (vec)
-      fg::slice_owner_kernel<true><<<grid, fg::kSliceBlock, 0, stream>>>(
-          values, ids, row_status, logits, stride, s->first_row, s->rows, o);
-    else
-      fg::slice_owner_kernel<false><<<grid, fg::kSliceBlock, 0, stream>>>(
-          values, ids, row_status, logits, stride, s->first_row, s->rows, o);
-  } else if (vec) {
+    launched = slice_owner_launch<2048>(s, logits, stride, batch_rows, values, ids, row_status, o,
+                                        vec, stream) ||
+               slice_owner_launch<4096>(s, logits, stride, batch_rows, values, ids, row_status, o,
+                                        vec, stream) ||
+               slice_owner_launch<8192>(s, logits, stride, batch_rows, values, ids, row_status, o,
+                                        vec, stream);
+  }
+  if (launched) return hipGetLastError();
+  if (vec) {
     fg::slice_row_kernel<true><<<batch_rows, fg::kRowBlock, 0, stream>>>(
         values, ids, row_status, logits, stride, s->first_row, s->rows, o);
   } else {

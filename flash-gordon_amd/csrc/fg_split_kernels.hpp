@@ -13,7 +13,7 @@
 namespace fg {
 
 constexpr uint32_t kSliceBlock = 256;
-constexpr uint32_t kSliceChunk = 8192;  // logits per workgroup: 8 float4 per thread
+constexpr uint32_t kSliceWordStride = kWave;  // hand-off words per row: chunks <= 64
 constexpr uint32_t kSplitWaysMax = 4;
 constexpr int32_t kStatusMismatch = 5;  // FG_ERR_MISMATCH
 
@@ -24,8 +24,8 @@ struct SplitSpans {
 };
 
 // The best composite key (greedy_comp order, ids first_row + position) of
-// logits [base, base + kSliceChunk) of one row, in every thread.
-template <bool kVec>
+// logits [base, base + kChunk) of one row, in every thread.
+template <bool kVec, uint32_t kChunk>
 __device__ __forceinline__ uint64_t slice_chunk_best(const float* x, uint32_t base,
                                                      uint32_t slice_rows, uint32_t first_row,
                                                      uint64_t* s_best) {
@@ -43,7 +43,7 @@ __device__ __forceinline__ uint64_t slice_chunk_best(const float* x, uint32_t ba
     best_pos = take ? pos : best_pos;
   };
   if (kVec) {
-    constexpr uint32_t kLoads = kSliceChunk / (4u * kSliceBlock);
+    constexpr uint32_t kLoads = kChunk / (4u * kSliceBlock);
     float4 q[kLoads];
 #pragma unroll
     for (uint32_t l = 0; l < kLoads; l++) {
@@ -90,7 +90,7 @@ __device__ __forceinline__ uint64_t slice_chunk_best(const float* x, uint32_t ba
       }
     }
   } else {
-    const uint32_t end = min(base + kSliceChunk, slice_rows);
+    const uint32_t end = min(base + kChunk, slice_rows);
     for (uint32_t i = base + threadIdx.x; i < end; i += kSliceBlock) visit(x[i], i);
   }
   uint64_t best = best_key && best_pos < slice_rows
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256) void split_combine_kernel(
 // The owner's step: where the tagged hand-off's words and epochs live, and the
 // combine's inputs (combine != 0).
 struct SliceOwner {
-  uint64_t* words;   // [row * chunks + c]
+  uint64_t* words;   // [row * kSliceWordStride + c]
   uint32_t* epochs;  // [row] launches of the row finished
   uint32_t wait_ticks;  // chunk 0's wait limit, s_memrealtime ticks (100 MHz)
   uint32_t combine;     // 1: combine with the other ways' finalists
@@ -308,10 +308,12 @@ __global__ __launch_bounds__(kRowBlock) void slice_row_kernel(
 // with the other ways' finalists (loaded when it starts).  The epoch of row r
 // is epochs[r] % 8191 + 1, read by every chunk when it starts; the finisher
 // advances epochs[r] once it has every word (or has given up), so a word
-// left from an earlier launch always carries an older epoch, and replays of
+// left from an earlier launch always carries an older epoch (a row's words sit
+// at a fixed stride, so launches with another chunk size never alias them
+// with another row's), and replays of
 // a captured launch stay exact.
 
-template <bool kVec>
+template <bool kVec, uint32_t kChunk>
 __global__ __launch_bounds__(kSliceBlock) void slice_owner_kernel(
     float* values, uint32_t* ids, int32_t* row_status, const float* logits, uint64_t stride,
     uint32_t first_row, uint32_t slice_rows, SliceOwner o) {
@@ -325,10 +327,10 @@ __global__ __launch_bounds__(kSliceBlock) void slice_owner_kernel(
   if (o.combine && chunk == fin && threadIdx.x == 0u)
     parts = load_parts(row, o.part_values, o.part_ids, o.part_ranks, o.ways);
   const float* x = logits + static_cast<uint64_t>(row) * stride;
-  const uint64_t best = slice_chunk_best<kVec>(x, chunk * kSliceChunk, slice_rows, first_row, s_best);
+  const uint64_t best = slice_chunk_best<kVec, kChunk>(x, chunk * kChunk, slice_rows, first_row, s_best);
   if (threadIdx.x >= static_cast<uint32_t>(kWave)) return;
   const uint64_t header = wire_header(launches % kMaxEpoch + 1u);
-  uint64_t* const words = o.words + static_cast<uint64_t>(row) * chunks;
+  uint64_t* const words = o.words + static_cast<uint64_t>(row) * kSliceWordStride;
   if (chunk != fin) {
     if (lane == 0u)
       __hip_atomic_store(words + chunk, header | greedy_payload(best), __ATOMIC_RELAXED,

@@ -244,7 +244,7 @@ def _step_two_launches(dev, sl, x, vals, ids, ranks, ways, vocab, spans):
 @pytest.mark.parametrize("ways,rows", [(4, 64), (2, 64), (4, 5)])
 def test_slice_step_matches_reduce_then_combine(dev, ways, rows):
     """fg_hip_output_slice_reduce_combine (one launch, tagged hand-off to
-    chunk 0, combine in the same workgroup) against the two entry points it
+    the row's last chunk, which combines) against the two entry points it
     fuses, and against the oracle's combine of the oracle's finalist; three
     calls on one slice with new inputs each."""
     spans = [fg_hip.split_span(ways, w) for w in range(ways)]
@@ -309,8 +309,30 @@ def test_slice_step_graph_replays(dev):
             assert got_s[r] == ws and got_t[r] == wt, (rep, r)
 
 
+def test_slice_step_batches_switch_chunk_size(dev):
+    """Batches of 64, 200 and 400 rows on one slice take grids of 2,048-,
+    4,096- and 8,192-logit chunks (the smallest resident at once); calls that
+    switch between them stay exact against the oracle (a row's hand-off words
+    sit at a fixed stride, so no layout reads another row's words)."""
+    ways = 4
+    spans = [fg_hip.split_span(ways, w) for w in range(ways)]
+    first, n = spans[0]
+    sl = fg_hip.OutputSlice(Q38, ways, first, n, 400)
+    for call, rows in enumerate((64, 200, 400, 64, 200, 64)):
+        rng = np.random.default_rng(700 + call)
+        x = _rows(rng, rows, n)
+        vals, ids, ranks = _parts(rng, rows, ways, Q38, spans)
+        tok, _, st = _step(dev, sl, x, vals, ids, ranks, spans)
+        ov, oi, _ = O.slice_finalists(x, first)
+        for r in range(rows):
+            v, i = vals[r].copy(), ids[r].copy()
+            v[0], i[0] = ov[r], oi[r]
+            ws, wt, _ = O.split_combine_row(v, i, ranks[r], ways, Q38, spans)
+            assert st[r] == ws and tok[r] == wt, (call, rows, r)
+
+
 def test_slice_wait_limit_reports_and_next_call_is_exact(dev):
-    """A wait limit of 0: chunk 0 gives up on any word not yet there (status
+    """A wait limit of 0: the row's last chunk gives up on any word not yet there (status
     FG_ERR_UNAVAILABLE, token 0xffffffff) or finishes exactly; the next call,
     with the limit back, is exact."""
     ways, rows = 4, 64
