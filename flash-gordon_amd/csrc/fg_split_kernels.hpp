@@ -321,8 +321,11 @@ __global__ __launch_bounds__(kSliceBlock) void slice_owner_kernel(
   const uint32_t row = blockIdx.y, chunk = blockIdx.x, chunks = gridDim.x;
   const uint32_t fin = chunks - 1u;
   const uint32_t lane = lane_id();
-  const uint32_t launches =
-      __hip_atomic_load(o.epochs + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // A plain load: only an earlier launch writes the row's epoch (this one's
+  // finisher advances it after every chunk has read it and published), and
+  // the kernel boundary makes that store visible.  A device-scope load here
+  // would hold up the chunk's first data loads behind its longer round trip.
+  const uint32_t launches = o.epochs[row];
   RowParts parts{};
   if (o.combine && chunk == fin && threadIdx.x == 0u)
     parts = load_parts(row, o.part_values, o.part_ids, o.part_ranks, o.ways);
