@@ -680,6 +680,10 @@ fg_status fg_hip_topk_reduce_all(float* output_scores, uint32_t* output_ids,
   return FG_OK;
 }
 
+// Chunk layouts of the owner step's tagged hand-off: 2,048, 4,096 and 8,192
+// logits a workgroup.
+constexpr uint32_t kSliceLayouts = 3;
+
 struct fg_hip_output_slice {
   uint32_t vocab, ways, first_row, rows, max_batch;
   unsigned long long* d_keys;  // per batch row; zero between calls
@@ -722,11 +726,13 @@ fg_status fg_hip_output_slice_create(fg_hip_output_slice** out, uint32_t vocab, 
   if (e == hipSuccess) e = hipMemset(s->d_keys, 0, sizeof(unsigned long long) * max_batch_rows);
   if (e == hipSuccess) e = hipMemset(s->d_arrivals, 0, sizeof(uint32_t) * max_batch_rows);
   {
-    const size_t words = sizeof(uint64_t) * fg::kSliceWordStride * max_batch_rows;
+    // Words and epochs for each of the owner step's chunk layouts.
+    const size_t words = sizeof(uint64_t) * fg::kSliceWordStride * max_batch_rows * kSliceLayouts;
+    const size_t epochs = sizeof(uint32_t) * max_batch_rows * kSliceLayouts;
     if (e == hipSuccess) e = hipMalloc(&s->d_words, words);
-    if (e == hipSuccess) e = hipMalloc(&s->d_epochs, sizeof(uint32_t) * max_batch_rows);
+    if (e == hipSuccess) e = hipMalloc(&s->d_epochs, epochs);
     if (e == hipSuccess) e = hipMemset(s->d_words, 0, words);
-    if (e == hipSuccess) e = hipMemset(s->d_epochs, 0, sizeof(uint32_t) * max_batch_rows);
+    if (e == hipSuccess) e = hipMemset(s->d_epochs, 0, epochs);
     s->wait_ticks = static_cast<uint32_t>(
         std::min<uint64_t>(UINT32_MAX, tuning_from_env().wait_us * 100u));
   }
@@ -833,15 +839,22 @@ bool split_spans(uint32_t ways, uint32_t vocab, const uint32_t* span_first,
   return cursor == vocab;
 }
 
-// The tagged owner step with kChunk logits per workgroup, if its grid has
-// at most kSliceWordStride chunks a row and is resident at once.
+// The tagged owner step with kChunk logits per workgroup (chunk layout
+// `layout`), if its grid has at most kSliceWordStride chunks a row and is
+// resident at once.  Each layout has its own words and epochs: a launch
+// then rewrites every word its finishers poll, so a word's previous tag is
+// always the previous epoch of the same row and layout (with one shared set,
+// a word that a layout of fewer chunks leaves alone could keep a tag until
+// the row's epoch wraps back to it).
 template <uint32_t kChunk>
 bool slice_owner_launch(fg_hip_output_slice* s, const float* logits, uint64_t stride,
                         uint32_t batch_rows, float* values, uint32_t* ids, int32_t* row_status,
-                        const fg::SliceOwner& o, bool vec, hipStream_t stream) {
+                        fg::SliceOwner o, uint32_t layout, bool vec, hipStream_t stream) {
   const dim3 grid((s->rows + kChunk - 1u) / kChunk, batch_rows);
   if (grid.x > fg::kSliceWordStride || !slice_grid_resident<kChunk>(grid.x * grid.y))
     return false;
+  o.words = s->d_words + static_cast<size_t>(layout) * fg::kSliceWordStride * s->max_batch;
+  o.epochs = s->d_epochs + static_cast<size_t>(layout) * s->max_batch;
   if (vec)
     fg::slice_owner_kernel<true, kChunk><<<grid, fg::kSliceBlock, 0, stream>>>(
         values, ids, row_status, logits, stride, s->first_row, s->rows, o);
@@ -862,15 +875,13 @@ hipError_t slice_step(fg_hip_output_slice* s, const float* logits, uint64_t stri
   const bool vec = aligned16(logits) && stride % 4u == 0u && s->rows % 4u == 0u;
   bool launched = false;
   if (static_cast<uint64_t>(s->first_row) + s->rows <= fg::kWireVocab) {
-    o.words = s->d_words;
-    o.epochs = s->d_epochs;
     o.wait_ticks = s->wait_ticks;
     launched = slice_owner_launch<2048>(s, logits, stride, batch_rows, values, ids, row_status, o,
-                                        vec, stream) ||
+                                        0u, vec, stream) ||
                slice_owner_launch<4096>(s, logits, stride, batch_rows, values, ids, row_status, o,
-                                        vec, stream) ||
+                                        1u, vec, stream) ||
                slice_owner_launch<8192>(s, logits, stride, batch_rows, values, ids, row_status, o,
-                                        vec, stream);
+                                        2u, vec, stream);
   }
   if (launched) return hipGetLastError();
   if (vec) {

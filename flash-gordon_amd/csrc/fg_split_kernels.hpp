@@ -324,10 +324,11 @@ __global__ __launch_bounds__(kRowBlock) void slice_row_kernel(
 // with the other ways' finalists (loaded when it starts).  The epoch of row r
 // is epochs[r] % 8191 + 1, read by every chunk when it starts; the finisher
 // advances epochs[r] once it has every word (or has given up), so a word
-// left from an earlier launch always carries an older epoch (a row's words sit
-// at a fixed stride, so launches with another chunk size never alias them
-// with another row's), and replays of
-// a captured launch stay exact.
+// left from an earlier launch always carries an older epoch, and replays of
+// a captured launch stay exact.  The words and epochs passed in belong to
+// this launch's chunk size (the host keeps a set per size, a row's words at a
+// fixed stride), so every word a finisher polls was written by the previous
+// launch of the same row and size.
 
 template <bool kVec, uint32_t kChunk>
 __global__ __launch_bounds__(kSliceBlock) void slice_owner_kernel(

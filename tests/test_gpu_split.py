@@ -331,6 +331,43 @@ def test_slice_step_batches_switch_chunk_size(dev):
             assert st[r] == ws and tok[r] == wt, (call, rows, r)
 
 
+def test_slice_step_layout_words_survive_epoch_wrap(dev):
+    """A 64-row call (2,048-logit chunks, 19 words a row) leaves large bests
+    in words 10-17; 8,190 calls of 200 rows (4,096-logit chunks, 10 words)
+    then bring rows 0-63's epoch round to the first call's tag.  The next
+    64-row call, on smaller logits, must not take those words: each chunk
+    layout has its own words and epochs."""
+    import torch
+    ways = 4
+    spans = [fg_hip.split_span(ways, w) for w in range(ways)]
+    first, n = spans[0]
+    sl = fg_hip.OutputSlice(Q38, ways, first, n, 200)
+    rng = np.random.default_rng(808)
+    xc = _rows(rng, 64, n, specials=False)
+    vals, ids, ranks = _parts(rng, 64, ways, Q38, spans, bad=False)
+    _step(dev, sl, xc + np.float32(100.0), vals, ids, ranks, spans)  # tags epoch 1
+    rows = 200
+    xb = _rows(rng, rows, n, specials=False)
+    vb, ib, rb = _parts(rng, rows, ways, Q38, spans, bad=False)
+    tx = torch.from_numpy(xb).to(dev)
+    tv, ti, tr = (torch.from_numpy(vb).to(dev), torch.from_numpy(ib.view(np.int32)).to(dev),
+                  torch.from_numpy(rb).to(dev))
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    lg = torch.empty(rows, dtype=torch.float32, device=dev)
+    st = torch.empty(rows, dtype=torch.int32, device=dev)
+    for _ in range(8190):
+        sl.reduce_combine(tx, tv, ti, tr, spans, tok, lg, st)
+    torch.cuda.synchronize()
+    assert int(st.abs().sum()) == 0
+    got_t, _, got_s = _step(dev, sl, xc, vals, ids, ranks, spans)
+    ov, oi, _ = O.slice_finalists(xc, first)
+    for r in range(64):
+        v, i = vals[r].copy(), ids[r].copy()
+        v[0], i[0] = ov[r], oi[r]
+        ws, wt, _ = O.split_combine_row(v, i, ranks[r], ways, Q38, spans)
+        assert got_s[r] == ws and got_t[r] == wt, r
+
+
 def test_slice_wait_limit_reports_and_next_call_is_exact(dev):
     """A wait limit of 0: the row's last chunk gives up on any word not yet there (status
     FG_ERR_UNAVAILABLE, token 0xffffffff) or finishes exactly; the next call,
